@@ -1,0 +1,221 @@
+"""Throughput of the Laya encoder + decision-head forward pass on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--no-cpu-baseline]
+
+Workload (default, "c3"): ModernBERT-large encoder + 2-layer decision head, bf16, batch 32,
+sequence lengths uniform in [32, 512] (seed 0, packed without padding), 4 option markers per
+question, random-init N(0, 0.02) weights from the seeded generator.  A step is one full forward
+pass of that batch (embeddings, 28 encoder layers, head, scorer, act head).
+
+Timed region: K back-to-back replays of the pass (HIP graph, inputs resident in HBM; only the
+pass's few-KB index arrays are re-copied from pinned memory), bracketed by
+torch.cuda.synchronize().  `abi_seqs_per_s` times the same K steps through laya_forward_batch
+(host packing, H2D/D2H and synchronisation included).
+
+roofline: per-stage device times come from HIP events on the engine's stream
+(laya_ext_prof_enable); the dominant kernel's achieved rate is its algorithmic work per launch
+(2*M*N*K flops for a GEMM over the valid tokens) divided by its average launch time.
+
+cpu_baseline: the CPU PyTorch restatement of the same forward pass (oracle/model.py, fp32) on
+the first questions of the same batch, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+PEAK_BF16 = 2.5e15
+PEAK_FP32 = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def stage_work(name, cfg, T, R, KT, B, elt, attn_flops):
+    """Algorithmic (flops, bytes) of one launch of a stage; R/KT/B only for the head-1 stages."""
+    D, I, FF = cfg.d, cfg.intermediate, cfg.head_ffn
+    g = lambda m, n, k: (2.0 * m * n * k, float(elt * (m * k + n * k + m * n)))
+    table = {
+        "enc:gemm_qkv_rope": g(T, 3 * D, D),
+        "enc:gemm_attn_out_res": g(T, D, D),
+        "enc:gemm_mlp_in_geglu": g(T, 2 * I, D),
+        "enc:gemm_mlp_out_res": g(T, D, I),
+        "head:gemm_qkv": g(T, 3 * D, D),
+        "scorer:gemm_gelu": g(KT, D, D),
+        "enc:embed_ln": (0.0, float(T * D * (elt + 4 + elt))),
+        "enc:ln": (0.0, float(T * D * (4 + elt))),
+        "enc:final_ln_type": (0.0, float(T * D * 8)),
+        "enc:attn_sliding": (attn_flops["sliding"], float(T * D * 4 * elt)),
+        "enc:attn_global": (attn_flops["global"], float(T * D * 4 * elt)),
+    }
+    return table.get(name)
+
+
+def attention_flops(lens, D, half_window):
+    """4*D flops per (query, visible key) pair: QK^T and PV, all heads."""
+    s_glob = s_slide = 0
+    for L in lens:
+        p = np.arange(L)
+        s_glob += L * L
+        s_slide += int((np.minimum(L, p + half_window + 1) - np.maximum(0, p - half_window)).sum())
+    return {"global": 4.0 * D * s_glob, "sliding": 4.0 * D * s_slide}
+
+
+def cpu_baseline(cfg_name, batch, budget_s=20.0):
+    import torch
+    from layamd_amd import checkpoint as ck
+    from oracle import model as om
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg, W = ck.load_checkpoint(ck.cached_checkpoint(batch.cfg.name))
+    Wt = om.Weights(W)
+    idx, n_tok, t_used = [], 0, 0.0
+    t0 = time.time()
+    for i in range(batch.B):
+        t = time.time()
+        om.run_batch(Wt, batch.cfg, batch.subset([i]))
+        t_used += time.time() - t
+        idx.append(i)
+        n_tok += int(batch.lens[i])
+        if time.time() - t0 > budget_s:
+            break
+    return {"value": round(len(idx) / t_used, 4), "unit": "seqs/s", "cores": threads, "kind": "port",
+            "tokens_per_s": round(n_tok / t_used, 1),
+            "sample": "first %d of the %d questions (%d tokens), fp32 torch CPU restatement (oracle/model.py), "
+                      "one question per forward like the engine's packing" % (len(idx), batch.B, n_tok)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "c1"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the decision pass is data parallel with no cross-GPU exchange, "
+              "so only --gpus 1 is supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from layamd_amd import checkpoint as ck
+    from layamd_amd import engine as le
+    from layamd_amd import workloads as wl
+
+    batch = wl.CONFIGS[a.config](0)
+    cfg = batch.cfg
+    precision = batch.dtype
+    elt = 2 if precision == "bf16" else 4
+    t0 = time.time()
+    mdir = ck.cached_checkpoint(cfg.name)
+    print("[bench] checkpoint %s ready in %.1fs" % (mdir, time.time() - t0), file=sys.stderr, flush=True)
+    max_tokens = max(16384, int(batch.tokens) + 1024)
+    eng = le.Engine(None, mdir, precision=precision, env={"LAYA_MAX_TOKENS": max_tokens, "LAYA_GRAPHS": 1,
+                                                         "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None})
+    flat = batch.flat()
+    for _ in range(max(1, a.warmup)):
+        eng.forward_flat(*flat)
+    torch.cuda.synchronize()
+
+    # timed region: K device-resident replays of the pass
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    dev_ms = eng.replay(a.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t
+    ms_per_step = 1000.0 * wall / a.steps
+    seqs_s = batch.B * a.steps / wall
+    tok_s = batch.tokens * a.steps / wall
+
+    # same K steps through the C ABI (host packing + copies included)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(a.steps):
+        eng.forward_flat(*flat)
+    torch.cuda.synchronize()
+    abi_wall = time.perf_counter() - t
+    print("[bench] %s: %.3f ms/step (device %.3f ms), %.1f seqs/s, %.0f tok/s; ABI %.3f ms/step"
+          % (a.config, ms_per_step, dev_ms / a.steps, seqs_s, tok_s, 1000 * abi_wall / a.steps),
+          file=sys.stderr, flush=True)
+
+    # per-stage device times (event-bracketed, graphs bypassed)
+    eng.prof_enable(True)
+    eng.prof_reset()
+    n_prof = 3
+    for _ in range(n_prof):
+        eng.forward_flat(*flat)
+    stages = eng.prof_stages()
+    eng.prof_enable(False)
+    eng.prof_report(n_prof)
+    sys.stdout.flush()
+
+    T, B, KT = batch.tokens, batch.B, int(batch.nmark.sum())
+    R = KT + B
+    af = attention_flops(batch.lens, cfg.d, cfg.local_attention // 2)
+    kernels = {}
+    gemm_flops = gemm_ms = 0.0
+    for name, (ms, calls) in stages.items():
+        w = stage_work(name, cfg, T, R, KT, B, elt, af)
+        avg_ms = ms / calls
+        entry = {"ms_per_launch": round(avg_ms, 5), "launches_per_step": calls // n_prof}
+        if w is not None:
+            fl, by = w
+            if fl and "gemm" in name:
+                entry["tflops"] = round(fl / (avg_ms * 1e-3) / 1e12, 1)
+                entry["frac_mfma"] = round(fl / (avg_ms * 1e-3) / (PEAK_BF16 if elt == 2 else PEAK_FP32), 4)
+                if name.startswith("enc:"):
+                    gemm_flops += fl * calls
+                    gemm_ms += ms
+            else:
+                entry["gbs"] = round(by / (avg_ms * 1e-3) / 1e9, 1)
+                entry["frac_hbm"] = round(by / (avg_ms * 1e-3) / PEAK_HBM, 4)
+                if fl:
+                    entry["tflops"] = round(fl / (avg_ms * 1e-3) / 1e12, 1)
+        kernels[name] = entry
+    dom = max((n for n in stages if stage_work(n, cfg, T, R, KT, B, elt, af) is not None), key=lambda n: stages[n][0])
+    fl, by = stage_work(dom, cfg, T, R, KT, B, elt, af)
+    dom_ms = stages[dom][0] / stages[dom][1]
+    if fl and "gemm" in dom:
+        ach = fl / (dom_ms * 1e-3) / 1e12
+        peak = (PEAK_BF16 if elt == 2 else PEAK_FP32) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(ach / peak, 4), "traffic": None, "kernel": dom,
+                "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T)}
+    else:
+        ach = by / (dom_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": None, "kernel": dom}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(a.config, batch, a.cpu_budget)
+
+    line = {
+        "metric": "seqs/s & tokens/s, ModernBERT-large bf16 b32xs512, 1 GPU; GEMM MFMA util %"
+                  if a.config == "c3" else "seqs/s (%s)" % batch.name,
+        "value": round(seqs_s, 2), "unit": "seqs/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": precision, "data": "synthetic (seeded token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": batch.name, "model": cfg.name, "layers": cfg.n_layers, "d_model": cfg.d,
+                   "global_batch": batch.B, "seq_len": int(cfg.max_len), "valid_tokens": T,
+                   "markers": KT, "parallelism": "single GPU"},
+        "tokens_per_s": round(tok_s, 1),
+        "padded_slots_per_s": round(batch.B * cfg.max_len * a.steps / wall, 1),
+        "abi_seqs_per_s": round(batch.B * a.steps / abi_wall, 2),
+        "mfma_util_encoder_gemms": round(gemm_flops / (gemm_ms * 1e-3) / (PEAK_BF16 if elt == 2 else PEAK_FP32), 4)
+        if gemm_ms else None,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

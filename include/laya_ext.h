@@ -1,0 +1,39 @@
+/* Measurement hooks of the MI355X Laya engine.  None of these has a counterpart in the reference
+ * ABI (src/laya_api.h); they exist for benchmarking and debugging and are not needed by the
+ * reference's callers. */
+#pragma once
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Turns per-stage event timing on (1) or off (0) at run time.  While on, every stage is bracketed
+ * by HIP events on the engine's stream and synchronised, and HIP graphs are bypassed.  Returns the
+ * previous state. */
+int laya_ext_prof_enable(void* h, int on);
+
+/* Stage i of the profile table: copies its name (NUL-terminated, at most name_len bytes), total
+ * device milliseconds and number of launches.  Returns 0, or -1 when i is out of range. */
+int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, long long* calls);
+
+/* Re-runs the most recent pass `iters` times exactly as laya_forward_batch runs it (graph replay
+ * when graphs are on) and stores the device time of all iterations, measured with HIP events on
+ * the engine's stream, in *ms.  Inputs stay resident; only the pass's small index arrays are
+ * re-copied from pinned host memory.  Returns 0, or -1 when no pass has run yet. */
+int laya_ext_replay(void* h, int iters, float* ms);
+
+/* "bf16" or "fp32": the storage type of GEMM and attention operands (LAYA_PRECISION). */
+const char* laya_ext_precision(void* h);
+
+/* The engine's MFMA GEMM on caller-owned device buffers: C[M,N] = A[M,K] . W[N,K]^T.
+ * dtype 0: fp32 operands, 1: bf16 operands (fp32 accumulate in both).
+ * epi 0: C (dtype) = act(result + bias), act 0 none / 1 ReLU / 2 GELU;
+ * epi 1: C is fp32 and C += result + bias.  bias is fp32 [N] or NULL.
+ * Runs `iters` (>= 1) launches on `stream` (a hipStream_t, NULL = default stream); when ms is
+ * non-NULL stores their total device time from HIP events.  Returns 0, or -1 when the shape or
+ * alignment is not supported (K a multiple of 64 bf16 / 32 fp32 elements, 16-byte aligned rows). */
+int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
+                  int K, void* stream, int iters, float* ms);
+
+#ifdef __cplusplus
+}
+#endif

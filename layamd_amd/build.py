@@ -1,0 +1,86 @@
+"""Builds the engine in-tree:
+
+    layamd_amd/liblaya.so       the laya_api.h C ABI + gfx950 kernels (hipcc --offload-arch=gfx950)
+    layamd_amd/liblaya_host.so  host-only packer/loader entry points for the CPU tests (g++)
+
+    python -m layamd_amd.build [--jobs N]
+
+Each translation unit is compiled separately (in parallel) into layamd_amd/_build/, then linked.
+HIP code is built with packed-fp32 instruction generation disabled.
+"""
+import argparse
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "liblaya.so")
+HOST_LIB = os.path.join(PKG, "liblaya_host.so")
+
+HIP_SOURCES = ["engine.hip", "kernels_gemm.hip", "kernels_attn.hip", "kernels_norm.hip"]
+CPP_SOURCES = ["model.cpp", "pack.cpp"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-I" + CSRC, "-I" + INCLUDE,
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result"]
+CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-I" + CSRC, "-I" + INCLUDE, "-Wall"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError("build step failed: %s\n%s" % (" ".join(cmd), out))
+    return out
+
+
+def _newer(target, deps):
+    if not os.path.exists(target):
+        return False
+    t = os.path.getmtime(target)
+    return all(os.path.getmtime(d) <= t for d in deps)
+
+
+def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + \
+              [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+    steps = []
+    for s in HIP_SOURCES:
+        src, obj = os.path.join(CSRC, s), os.path.join(BUILD, s + ".o")
+        steps.append((obj, [src] + headers, [HIPCC] + HIP_FLAGS + ["-c", src, "-o", obj]))
+    for s in CPP_SOURCES:
+        src, obj = os.path.join(CSRC, s), os.path.join(BUILD, s + ".o")
+        steps.append((obj, [src] + headers, ["g++"] + CXX_FLAGS + ["-c", src, "-o", obj]))
+    todo = [st for st in steps if force or not _newer(st[0], st[1])]
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        for out in ex.map(lambda st: _run(st[2]), todo):
+            if out.strip() and verbose:
+                print(out)
+    objs = [st[0] for st in steps]
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"])
+    os.replace(tmp, LIB)
+    tmp = HOST_LIB + ".tmp"
+    _run(["g++"] + CXX_FLAGS + ["-shared", "-o", tmp, os.path.join(CSRC, "host_probe.cpp"),
+                                os.path.join(CSRC, "model.cpp"), os.path.join(CSRC, "pack.cpp")])
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print("[build] %s\n[build] %s" % (LIB, HOST_LIB))
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--incremental", action="store_true")
+    a = ap.parse_args()
+    try:
+        build(a.jobs, force=not a.incremental)
+    except RuntimeError as e:
+        print(e, file=sys.stderr)
+        sys.exit(1)

@@ -1,0 +1,50 @@
+// Shared device/host helpers for the gfx950 Laya engine: error checks, the two element types
+// (bf16 storage with fp32 math, or fp32), and wave64 reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#define LAYA_HIP(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { \
+  fprintf(stderr, "[laya] HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); exit(1); } } while (0)
+
+namespace laya {
+
+typedef uint16_t bf16_t;                       // bf16 bit pattern in memory
+
+__host__ __device__ inline float bf2f(bf16_t b) {
+  union { uint32_t u; float f; } c; c.u = (uint32_t)b << 16; return c.f;
+}
+__host__ __device__ inline bf16_t f2bf(float f) {     // round to nearest even (finite inputs)
+  union { uint32_t u; float f; } c; c.f = f;
+  uint32_t r = ((c.u >> 16) & 1u) + 0x7FFFu;
+  return (bf16_t)((c.u + r) >> 16);
+}
+
+// Element-type traits: loads/stores of one element with fp32 math.
+template <typename T> struct Elt;
+template <> struct Elt<float> {
+  static __device__ __forceinline__ float ld(const float* p) { return *p; }
+  static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+};
+template <> struct Elt<bf16_t> {
+  static __device__ __forceinline__ float ld(const bf16_t* p) { return bf2f(*p); }
+  static __device__ __forceinline__ void st(bf16_t* p, float v) { *p = f2bf(v); }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// exact (erf) GELU, as torch.nn.functional.gelu with approximate="none"
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752440f)); }
+
+}  // namespace laya

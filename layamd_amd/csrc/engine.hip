@@ -1,0 +1,624 @@
+// Laya engine for AMD Instinct MI355X (gfx950): weight upload, pass execution, HIP graphs and the
+// laya_api.h C ABI.
+//
+// One pass runs a whole batch of questions packed densely (see pack.h), on one stream:
+//
+//   embeddings -> LN                                   k_layernorm (gather by token id)
+//   per encoder layer:
+//     QKV GEMM + RoPE + V^T write                      k_gemm<EPI_QKV>
+//     attention (global | sliding +-64)                k_attention
+//     out-proj GEMM, x += (fp32 residual)               k_gemm<EPI_RESID>
+//     LN -> xn                                         k_layernorm
+//     Wi GEMM + GeGLU                                  k_gemm<EPI_GEGLU>
+//     Wo GEMM, x +=                                    k_gemm<EPI_RESID>
+//     LN -> xn (next attn_norm) | final LN + type embedding into x
+//   head layer 0 (all rows), head layer 1 on the gathered marker + CLS rows, scorer, act head.
+//
+// Semantics follow the reference's Engine::run / forward_batch (src/engine.hip:396-539) and the
+// upstream model it serves (ref/rl_common.py:100-124); the kernels, data layout and fusion are
+// this engine's own (weights keep their [out, in] layout; RoPE, the V transpose and GeGLU are
+// GEMM epilogues; the residual add happens in the GEMM epilogue in fp32).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <thread>
+#include <tuple>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+#include "laya_api.h"
+#include "laya_ext.h"
+#include "model.h"
+#include "pack.h"
+
+namespace laya {
+
+static int env_int(const char* n, int d) { const char* s = getenv(n); return s && *s ? atoi(s) : d; }
+
+// ---------------------------------------------------------------- profiling
+struct Prof {
+  bool on = false;
+  hipEvent_t a = nullptr, b = nullptr;
+  std::vector<std::tuple<std::string, double, long long>> acc;
+  void init() {
+    LAYA_HIP(hipEventCreate(&a));
+    LAYA_HIP(hipEventCreate(&b));
+    const char* p = getenv("LAYA_PROFILE");
+    on = p != nullptr && *p && strcmp(p, "0") != 0;
+  }
+  void start(hipStream_t st) { if (on) LAYA_HIP(hipEventRecord(a, st)); }
+  void stop(const char* name, hipStream_t st) {
+    if (!on) return;
+    LAYA_HIP(hipEventRecord(b, st));
+    LAYA_HIP(hipEventSynchronize(b));
+    float ms = 0.f;
+    LAYA_HIP(hipEventElapsedTime(&ms, a, b));
+    for (auto& e : acc)
+      if (std::get<0>(e) == name) { std::get<1>(e) += ms; std::get<2>(e) += 1; return; }
+    acc.emplace_back(name, (double)ms, 1LL);
+  }
+  void report(int iters) {
+    if (acc.empty()) { printf("[laya] profile is empty (set LAYA_PROFILE or call laya_ext_prof_enable)\n"); return; }
+    if (iters < 1) iters = 1;
+    double tot = 0;
+    for (auto& e : acc) tot += std::get<1>(e);
+    auto v = acc;
+    std::sort(v.begin(), v.end(), [](auto& x, auto& y) { return std::get<1>(x) > std::get<1>(y); });
+    printf("\n%-28s %10s %8s %7s\n", "stage", "ms/fwd", "calls", "%");
+    for (auto& e : v)
+      printf("%-28s %10.4f %8lld %6.1f%%\n", std::get<0>(e).c_str(), std::get<1>(e) / iters, std::get<2>(e),
+             100.0 * std::get<1>(e) / tot);
+    printf("%-28s %10.4f (serialized sum)\n", "TOTAL", tot / iters);
+  }
+};
+
+// ---------------------------------------------------------------- engine interface
+struct EngineIface {
+  Config cfg;
+  Prof prof;
+  virtual ~EngineIface() {}
+  virtual int forward_batch(int B, const int* lens, const int* ids, const int* nmark, const int* markers,
+                            const int* qtypes, float* logits, float* act) = 0;
+  virtual int replay(int iters, float* ms) = 0;
+  virtual void warmup() = 0;
+  virtual const char* precision() const = 0;
+};
+
+template <typename T>
+struct Engine : EngineIface {
+  struct EncLayer { float* attn_norm = nullptr; T* Wqkv; T* Wo; float* mlp_norm; T* Wi; T* Wmo; };
+  struct HeadLayer { float *n1w, *n1b, *n2w, *n2b, *inB, *outB, *l1B, *l2B; T *inW, *outW, *l1W, *l2W; };
+
+  hipStream_t stream = nullptr;
+  PackLimits lim;
+  PassCaps caps{};
+  bool use_graphs = true, capturing = false, verbose = false;
+  const char* dump_dir = nullptr;
+
+  // weights
+  T* tok_emb = nullptr;
+  float *emb_norm = nullptr, *final_norm = nullptr, *type_emb = nullptr;
+  std::vector<EncLayer> enc;
+  std::vector<HeadLayer> head;
+  float *sc0w, *sc0b, *sc1b, *sc3w, *sc3b;
+  T* sc1W;
+  float *ah0W, *ah0b, *ah2W, *ah2b;
+  float *cos_g, *sin_g, *cos_l, *sin_l;
+
+  // activations
+  int64_t MT = 0, RG = 0, VTC = 0;
+  float *x = nullptr, *xg = nullptr, *d_logits = nullptr, *d_act = nullptr;
+  T *xn, *q, *k, *vt, *ao, *mg, *ff, *aog, *xng, *sh;
+
+  // per-pass index arrays: device + pinned host mirrors at fixed addresses (graph replay)
+  int *d_ids, *d_pos, *d_seq, *d_vcol, *d_soff, *d_vlen, *d_vbase, *d_qt, *d_nm, *d_moff, *d_gq, *d_grow;
+  int *h_ids, *h_pos, *h_seq, *h_vcol, *h_soff, *h_vlen, *h_vbase, *h_qt, *h_nm, *h_moff, *h_gq, *h_grow;
+  AttnTile *d_tiles, *d_gtiles, *h_tiles, *h_gtiles;
+  float *h_logits, *h_act;
+
+  struct Shape {
+    int rows, B, KT, R, VT, nt, ngt;
+    bool operator<(const Shape& o) const {
+      return std::tie(rows, B, KT, R, VT, nt, ngt) < std::tie(o.rows, o.B, o.KT, o.R, o.VT, o.nt, o.ngt);
+    }
+  };
+  std::map<Shape, hipGraphExec_t> graphs;
+  bool have_last = false;
+  Shape last{};
+
+  const char* precision() const override { return sizeof(T) == 2 ? "bf16" : "fp32"; }
+
+  // ------------------------------------------------------------ allocation helpers
+  template <typename U> U* dalloc(size_t n, bool zero = false) {
+    U* p = nullptr;
+    LAYA_HIP(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(U)));
+    if (zero) LAYA_HIP(hipMemset(p, 0, std::max<size_t>(n, 1) * sizeof(U)));
+    return p;
+  }
+  template <typename U> U* halloc(size_t n) {
+    U* p = nullptr;
+    LAYA_HIP(hipHostMalloc(&p, std::max<size_t>(n, 1) * sizeof(U), hipHostMallocDefault));
+    return p;
+  }
+
+  static const TensorView& must(const SafeTensors& st, const std::string& n) {
+    const TensorView* t = st.get(n);
+    if (!t) { fprintf(stderr, "[laya] missing tensor %s\n", n.c_str()); exit(1); }
+    return *t;
+  }
+  static void check_shape(const TensorView& t, std::vector<int64_t> s, const std::string& n) {
+    if (t.shape != s) {
+      fprintf(stderr, "[laya] tensor %s has an unexpected shape\n", n.c_str());
+      exit(1);
+    }
+  }
+  static std::vector<float> host_f32(const TensorView& t) {
+    std::vector<float> v((size_t)t.numel());
+    tensor_to_f32(t, v.data());
+    return v;
+  }
+  float* up_f32(const SafeTensors& st, const std::string& n, std::vector<int64_t> shape) {
+    const TensorView& t = must(st, n);
+    check_shape(t, shape, n);
+    std::vector<float> v = host_f32(t);
+    float* d = dalloc<float>(v.size());
+    LAYA_HIP(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return d;
+  }
+  // matrix [rows, cols] with stored row i taken from source row perm[i] (identity when empty)
+  T* up_mat(const SafeTensors& st, const std::string& n, int64_t rows, int64_t cols, const std::vector<int>& perm = {}) {
+    const TensorView& t = must(st, n);
+    check_shape(t, {rows, cols}, n);
+    std::vector<float> v = host_f32(t);
+    std::vector<T> o((size_t)(rows * cols));
+    auto work = [&](int64_t r0, int64_t r1) {
+      for (int64_t r = r0; r < r1; r++) {
+        const float* s = v.data() + (perm.empty() ? r : perm[r]) * cols;
+        T* d = o.data() + r * cols;
+        for (int64_t c = 0; c < cols; c++) {
+          if constexpr (sizeof(T) == 2) d[c] = f2bf(s[c]); else d[c] = s[c];
+        }
+      }
+    };
+    const int nth = rows * cols > (1 << 22) ? 8 : 1;
+    std::vector<std::thread> th;
+    for (int i = 0; i < nth; i++) th.emplace_back(work, rows * i / nth, rows * (i + 1) / nth);
+    for (auto& x : th) x.join();
+    T* d = dalloc<T>(o.size());
+    LAYA_HIP(hipMemcpy(d, o.data(), o.size() * sizeof(T), hipMemcpyHostToDevice));
+    return d;
+  }
+  // q and k rows of each head reordered d = [0..15, 32..47, 16..31, 48..63] (RoPE pairs adjacent)
+  std::vector<int> rope_perm() const {
+    const int D = cfg.d, HD = cfg.head_dim;
+    std::vector<int> p(3 * D);
+    for (int r = 0; r < 3 * D; r++) {
+      const int sec = r / D, e = r % D, h = e / HD, t = e % HD;
+      if (sec == 2) { p[r] = r; continue; }
+      const int blk = t / 16, off = t % 16;
+      const int d = blk == 0 ? off : blk == 1 ? 32 + off : blk == 2 ? 16 + off : 48 + off;
+      p[r] = sec * D + h * HD + d;
+    }
+    return p;
+  }
+  // Wi rows as alternating 16-row blocks of input rows and gate rows
+  std::vector<int> geglu_perm() const {
+    const int I = cfg.intermediate;
+    std::vector<int> p(2 * I);
+    for (int r = 0; r < 2 * I; r++) {
+      const int pair = r / 32, within = r % 32;
+      p[r] = within < 16 ? pair * 16 + within : I + pair * 16 + (within - 16);
+    }
+    return p;
+  }
+
+  // ------------------------------------------------------------ load
+  void load(const std::string& dir) {
+    std::string err;
+    if (!cfg.load(dir + "/encoder/config.json", dir + "/rl_agent_config.json", &err)) {
+      fprintf(stderr, "[laya] %s\n", err.c_str());
+      exit(1);
+    }
+    verbose = getenv("LAYA_VERBOSE") != nullptr;
+    printf("%s[laya] precision=%s (gfx950 MFMA path)\n", cfg.describe().c_str(), precision());
+    const int D = cfg.d, I = cfg.intermediate, FF = cfg.head_ffn, H = cfg.n_heads, HD = cfg.head_dim, V = cfg.vocab;
+    if (HD != 64 || D % 64 || I % 16 || cfg.head_layers < 1 || cfg.n_act < 1 || cfg.n_act > 256) {
+      fprintf(stderr, "[laya] unsupported model shape (needs head_dim 64, d %% 64 == 0, intermediate %% 16 == 0, "
+                      "head_layers >= 1)\n");
+      exit(1);
+    }
+    SafeTensors st;
+    if (!st.open(dir + "/model.safetensors", &err)) { fprintf(stderr, "[laya] %s\n", err.c_str()); exit(1); }
+
+    tok_emb = up_mat(st, "encoder.embeddings.tok_embeddings.weight", V, D);
+    emb_norm = up_f32(st, "encoder.embeddings.norm.weight", {D});
+    final_norm = up_f32(st, "encoder.final_norm.weight", {D});
+    type_emb = up_f32(st, "type_emb.weight", {3, D});
+    const std::vector<int> rp = rope_perm(), gp = geglu_perm();
+    enc.resize(cfg.n_layers);
+    for (int i = 0; i < cfg.n_layers; i++) {
+      const std::string p = "encoder.layers." + std::to_string(i) + ".";
+      if (st.get(p + "attn_norm.weight") || i > 0) enc[i].attn_norm = up_f32(st, p + "attn_norm.weight", {D});
+      enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D, rp);
+      enc[i].Wo = up_mat(st, p + "attn.Wo.weight", D, D);
+      enc[i].mlp_norm = up_f32(st, p + "mlp_norm.weight", {D});
+      enc[i].Wi = up_mat(st, p + "mlp.Wi.weight", 2 * I, D, gp);
+      enc[i].Wmo = up_mat(st, p + "mlp.Wo.weight", D, I);
+    }
+    head.resize(cfg.head_layers);
+    for (int i = 0; i < cfg.head_layers; i++) {
+      const std::string p = "head.layers." + std::to_string(i) + ".";
+      HeadLayer& h = head[i];
+      h.n1w = up_f32(st, p + "norm1.weight", {D}); h.n1b = up_f32(st, p + "norm1.bias", {D});
+      h.n2w = up_f32(st, p + "norm2.weight", {D}); h.n2b = up_f32(st, p + "norm2.bias", {D});
+      h.inW = up_mat(st, p + "self_attn.in_proj_weight", 3 * D, D);
+      h.inB = up_f32(st, p + "self_attn.in_proj_bias", {3 * D});
+      h.outW = up_mat(st, p + "self_attn.out_proj.weight", D, D);
+      h.outB = up_f32(st, p + "self_attn.out_proj.bias", {D});
+      h.l1W = up_mat(st, p + "linear1.weight", FF, D); h.l1B = up_f32(st, p + "linear1.bias", {FF});
+      h.l2W = up_mat(st, p + "linear2.weight", D, FF); h.l2B = up_f32(st, p + "linear2.bias", {D});
+    }
+    sc0w = up_f32(st, "scorer.0.weight", {D}); sc0b = up_f32(st, "scorer.0.bias", {D});
+    sc1W = up_mat(st, "scorer.1.weight", D, D); sc1b = up_f32(st, "scorer.1.bias", {D});
+    sc3w = up_f32(st, "scorer.3.weight", {1, D}); sc3b = up_f32(st, "scorer.3.bias", {1});
+    ah0W = up_f32(st, "act_head.0.weight", {256, D + 4}); ah0b = up_f32(st, "act_head.0.bias", {256});
+    ah2W = up_f32(st, "act_head.2.weight", {cfg.n_act, 256}); ah2b = up_f32(st, "act_head.2.bias", {cfg.n_act});
+
+    // RoPE tables [max_len][HD/2], as HF builds them (modeling_modernbert.py:136-163): fp32
+    // inverse frequencies theta^(-2i/HD), fp32 position products, cos/sin of those.
+    {
+      const int L = cfg.max_len, H2 = HD / 2;
+      std::vector<float> cg((size_t)L * H2), sg(cg.size()), cl(cg.size()), sl(cg.size());
+      for (int i = 0; i < H2; i++) {
+        const float ig = 1.0f / powf(cfg.rope_theta_global, (float)(2 * i) / (float)HD);
+        const float il = 1.0f / powf(cfg.rope_theta_local, (float)(2 * i) / (float)HD);
+        for (int p = 0; p < L; p++) {
+          const float fg = (float)p * ig, fl = (float)p * il;
+          cg[(size_t)p * H2 + i] = (float)cos((double)fg); sg[(size_t)p * H2 + i] = (float)sin((double)fg);
+          cl[(size_t)p * H2 + i] = (float)cos((double)fl); sl[(size_t)p * H2 + i] = (float)sin((double)fl);
+        }
+      }
+      auto upv = [&](std::vector<float>& v) {
+        float* d = dalloc<float>(v.size());
+        LAYA_HIP(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+        return d;
+      };
+      cos_g = upv(cg); sin_g = upv(sg); cos_l = upv(cl); sin_l = upv(sl);
+    }
+
+    // limits and buffers
+    lim.max_len = cfg.max_len;
+    lim.vocab = V;
+    lim.pass_tokens = std::max(env_int("LAYA_MAX_TOKENS", 65536), cfg.max_len);
+    lim.pass_tokens = std::min(std::max(env_int("LAYA_PASS_TOKENS", lim.pass_tokens), cfg.max_len), lim.pass_tokens);
+    lim.max_seqs = std::max(1, env_int("LAYA_MAX_SEQS", 512));
+    lim.max_grows = std::max(env_int("LAYA_MAX_GATHERED", 32768), kMaxMarkers + 1);
+    caps = pass_caps(lim);
+    MT = caps.rows; RG = caps.grows; VTC = (caps.vt_cols + 63) / 64 * 64;
+    x = dalloc<float>((size_t)MT * D);
+    xn = dalloc<T>((size_t)MT * D); q = dalloc<T>((size_t)MT * D); k = dalloc<T>((size_t)MT * D);
+    ao = dalloc<T>((size_t)MT * D);
+    vt = dalloc<T>((size_t)D * VTC, true);      // zeroed once: unread gaps must stay finite
+    mg = dalloc<T>((size_t)MT * I);
+    ff = dalloc<T>((size_t)std::max(MT, RG) * FF);
+    xg = dalloc<float>((size_t)RG * D);
+    aog = dalloc<T>((size_t)RG * D); xng = dalloc<T>((size_t)RG * D); sh = dalloc<T>((size_t)RG * D);
+    d_logits = dalloc<float>((size_t)RG);
+    d_act = dalloc<float>((size_t)lim.max_seqs * cfg.n_act);
+    h_logits = halloc<float>((size_t)RG);
+    h_act = halloc<float>((size_t)lim.max_seqs * cfg.n_act);
+    auto pair = [&](int** d, int** h, size_t n) { *d = dalloc<int>(n); *h = halloc<int>(n); };
+    pair(&d_ids, &h_ids, MT); pair(&d_pos, &h_pos, MT); pair(&d_seq, &h_seq, MT); pair(&d_vcol, &h_vcol, MT);
+    pair(&d_soff, &h_soff, lim.max_seqs + 1); pair(&d_vlen, &h_vlen, lim.max_seqs);
+    pair(&d_vbase, &h_vbase, lim.max_seqs); pair(&d_qt, &h_qt, lim.max_seqs);
+    pair(&d_nm, &h_nm, lim.max_seqs); pair(&d_moff, &h_moff, lim.max_seqs);
+    pair(&d_gq, &h_gq, RG); pair(&d_grow, &h_grow, RG);
+    d_tiles = dalloc<AttnTile>(caps.tiles); h_tiles = halloc<AttnTile>(caps.tiles);
+    d_gtiles = dalloc<AttnTile>(caps.gtiles); h_gtiles = halloc<AttnTile>(caps.gtiles);
+
+    LAYA_HIP(hipStreamCreate(&stream));
+    prof.init();
+    use_graphs = env_int("LAYA_GRAPHS", 1) != 0;
+    dump_dir = getenv("LAYA_DUMP_DIR");
+    if (dump_dir && !*dump_dir) dump_dir = nullptr;
+    LAYA_HIP(hipDeviceSynchronize());
+    printf("[laya] ready: rows/pass=%lld gathered rows/pass=%lld graphs=%d\n", (long long)MT, (long long)RG,
+           (int)use_graphs);
+  }
+
+  // ------------------------------------------------------------ one pass
+  void stage_inputs(const PassPlan& p) {
+    memcpy(h_ids, p.ids.data(), p.T * 4); memcpy(h_pos, p.pos.data(), p.T * 4);
+    memcpy(h_seq, p.seq.data(), p.T * 4); memcpy(h_vcol, p.vcol.data(), p.T * 4);
+    memcpy(h_soff, p.soff.data(), (p.B + 1) * 4); memcpy(h_vlen, p.vlen.data(), p.B * 4);
+    memcpy(h_vbase, p.vbase.data(), p.B * 4); memcpy(h_qt, p.qt.data(), p.B * 4);
+    memcpy(h_nm, p.nm.data(), p.B * 4); memcpy(h_moff, p.moff.data(), p.B * 4);
+    memcpy(h_gq, p.gq.data(), p.gq.size() * 4); memcpy(h_grow, p.grow.data(), p.R * 4);
+    memcpy(h_tiles, p.tiles.data(), p.tiles.size() * sizeof(AttnTile));
+    memcpy(h_gtiles, p.gtiles.data(), p.gtiles.size() * sizeof(AttnTile));
+  }
+
+  void dump(const char* name, const float* dev, size_t rows) {
+    if (!dump_dir || capturing) return;
+    LAYA_HIP(hipStreamSynchronize(stream));
+    std::vector<float> buf(rows * cfg.d);
+    LAYA_HIP(hipMemcpy(buf.data(), dev, buf.size() * 4, hipMemcpyDeviceToHost));
+    std::string fn = std::string(dump_dir) + "/" + name + ".bin";
+    FILE* f = fopen(fn.c_str(), "wb");
+    if (f) { fwrite(buf.data(), 4, buf.size(), f); fclose(f); }
+  }
+
+  GemmArgs gemm_args(const T* A, int lda, const T* W, int M, int N, int K, const float* bias) {
+    GemmArgs g;
+    g.A = A; g.lda = lda; g.W = W; g.ldw = K; g.M = M; g.N = N; g.K = K; g.bias = bias;
+    return g;
+  }
+
+  void run(const Shape& s) {
+    const int D = cfg.d, H = cfg.n_heads, HD = cfg.head_dim, I = cfg.intermediate, FF = cfg.head_ffn;
+    const float eps = cfg.norm_eps, scale = 1.0f / sqrtf((float)HD);
+    const int T_ = s.rows, B = s.B, KT = s.KT, R = s.R;
+    hipStream_t st = stream;
+    auto h2d = [&](void* d, const void* h, size_t n) { LAYA_HIP(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st)); };
+    h2d(d_ids, h_ids, T_ * 4); h2d(d_pos, h_pos, T_ * 4); h2d(d_seq, h_seq, T_ * 4); h2d(d_vcol, h_vcol, T_ * 4);
+    h2d(d_soff, h_soff, (B + 1) * 4); h2d(d_vlen, h_vlen, B * 4); h2d(d_vbase, h_vbase, B * 4);
+    h2d(d_qt, h_qt, B * 4); h2d(d_nm, h_nm, B * 4); h2d(d_moff, h_moff, B * 4);
+    h2d(d_gq, h_gq, R * 4); h2d(d_grow, h_grow, R * 4);
+    h2d(d_tiles, h_tiles, s.nt * sizeof(AttnTile)); h2d(d_gtiles, h_gtiles, s.ngt * sizeof(AttnTile));
+
+#define STAGE(name, ...) do { prof.start(st); __VA_ARGS__; prof.stop(name, st); } while (0)
+    STAGE("enc:embed_ln", launch_layernorm<T, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
+                                                 nullptr, x, enc[0].attn_norm ? nullptr : xn, st));
+    dump("emb", x, T_);
+    for (int L = 0; L < cfg.n_layers; L++) {
+      const EncLayer& e = enc[L];
+      const bool glob = cfg.global_layer[L] != 0;
+      if (L == 0 && e.attn_norm)
+        STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.attn_norm, nullptr, nullptr, nullptr,
+                                                   nullptr, nullptr, xn, st));
+      {
+        GemmArgs g = gemm_args(xn, D, e.Wqkv, T_, 3 * D, D, nullptr);
+        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos; g.vcol = d_vcol;
+        g.rope_cos = glob ? cos_g : cos_l; g.rope_sin = glob ? sin_g : sin_l;
+        STAGE("enc:gemm_qkv_rope", launch_gemm<T>(EPI_QKV, g, st));
+      }
+      STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
+            launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, d_vbase, nullptr,
+                                nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
+      {
+        GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
+        g.X = x; g.ldx = D;
+        STAGE("enc:gemm_attn_out_res", launch_gemm<T>(EPI_RESID, g, st));
+      }
+      STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.mlp_norm, nullptr, nullptr, nullptr, nullptr,
+                                                 nullptr, xn, st));
+      {
+        GemmArgs g = gemm_args(xn, D, e.Wi, T_, 2 * I, D, nullptr);
+        g.C = mg; g.ldc = I;
+        STAGE("enc:gemm_mlp_in_geglu", launch_gemm<T>(EPI_GEGLU, g, st));
+      }
+      {
+        GemmArgs g = gemm_args(mg, I, e.Wmo, T_, D, I, nullptr);
+        g.X = x; g.ldx = D;
+        STAGE("enc:gemm_mlp_out_res", launch_gemm<T>(EPI_RESID, g, st));
+      }
+      if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "enc%d", L); dump(nm, x, T_); }
+      if (L + 1 < cfg.n_layers) {
+        STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, enc[L + 1].attn_norm, nullptr, nullptr,
+                                                   nullptr, nullptr, nullptr, xn, st));
+      } else {
+        // final_norm then + type_emb[qtype of the row's question] (ref/rl_common.py:104), in place
+        STAGE("enc:final_ln_type", launch_layernorm<float, T>(x, nullptr, T_, D, eps, final_norm, nullptr, type_emb,
+                                                              d_qt, d_seq, x, (T*)nullptr, st));
+      }
+    }
+    dump("final", x, T_);
+
+    for (int L = 0; L < cfg.head_layers; L++) {
+      const HeadLayer& hl = head[L];
+      const bool last = L == cfg.head_layers - 1;
+      STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n1w, hl.n1b, nullptr, nullptr, nullptr,
+                                                  nullptr, xn, st));
+      {
+        GemmArgs g = gemm_args(xn, D, hl.inW, T_, 3 * D, D, hl.inB);
+        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos; g.vcol = d_vcol;
+        STAGE("head:gemm_qkv", launch_gemm<T>(EPI_QKV, g, st));
+      }
+      if (!last) {
+        STAGE("head:attn", launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, d_vbase,
+                                               nullptr, nullptr, 0, scale, st));
+        { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
+          STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
+        STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
+                                                    nullptr, xn, st));
+        { GemmArgs g = gemm_args(xn, D, hl.l1W, T_, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
+          STAGE("head:gemm_ffn1_relu", launch_gemm<T>(EPI_STORE, g, st)); }
+        { GemmArgs g = gemm_args(ff, FF, hl.l2W, T_, D, FF, hl.l2B); g.X = x; g.ldx = D;
+          STAGE("head:gemm_ffn2_res", launch_gemm<T>(EPI_RESID, g, st)); }
+        if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
+      } else {
+        // queries, out-proj and FFN only for the R = KT + B rows read afterwards
+        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
+                                                        d_vlen, d_vbase, d_gq, d_grow, 0, scale, st));
+        STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
+        { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D;
+          STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
+        STAGE("head:ln", launch_layernorm<float, T>(xg, nullptr, R, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
+                                                    nullptr, xng, st));
+        { GemmArgs g = gemm_args(xng, D, hl.l1W, R, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
+          STAGE("head:gemm_ffn1_relu", launch_gemm<T>(EPI_STORE, g, st)); }
+        { GemmArgs g = gemm_args(ff, FF, hl.l2W, R, D, FF, hl.l2B); g.X = xg; g.ldx = D;
+          STAGE("head:gemm_ffn2_res", launch_gemm<T>(EPI_RESID, g, st)); }
+        if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d_gathered", L); dump(nm, xg, R); }
+      }
+    }
+    // scorer on the KT marker rows: LN(+bias) -> Linear + GELU -> Linear(D -> 1)
+    STAGE("scorer:ln", launch_layernorm<float, T>(xg, nullptr, KT, D, eps, sc0w, sc0b, nullptr, nullptr, nullptr,
+                                                  nullptr, xng, st));
+    { GemmArgs g = gemm_args(xng, D, sc1W, KT, D, D, sc1b); g.C = sh; g.ldc = D; g.act = ACT_GELU;
+      STAGE("scorer:gemm_gelu", launch_gemm<T>(EPI_STORE, g, st)); }
+    STAGE("scorer:dot", launch_row_dot<T>(sh, D, sc3w, sc3b, d_logits, KT, D, st));
+    STAGE("act_head", launch_act_head(xg + (size_t)KT * D, D, d_logits, d_moff, d_nm, ah0W, ah0b, ah2W, ah2b,
+                                      cfg.n_act, d_act, B, st));
+#undef STAGE
+    LAYA_HIP(hipMemcpyAsync(h_logits, d_logits, (size_t)KT * 4, hipMemcpyDeviceToHost, st));
+    LAYA_HIP(hipMemcpyAsync(h_act, d_act, (size_t)B * cfg.n_act * 4, hipMemcpyDeviceToHost, st));
+  }
+
+  // graph replay on a hit; on a miss run eagerly, then capture the same sequence
+  void execute(const Shape& s) {
+    last = s; have_last = true;
+    const bool graphs_on = use_graphs && !prof.on && !dump_dir;
+    if (graphs_on) {
+      auto it = graphs.find(s);
+      if (it != graphs.end()) {
+        LAYA_HIP(hipGraphLaunch(it->second, stream));
+        LAYA_HIP(hipStreamSynchronize(stream));
+        return;
+      }
+    }
+    run(s);
+    LAYA_HIP(hipStreamSynchronize(stream));
+    if (!graphs_on || graphs.size() >= 512) return;
+    hipGraph_t g;
+    hipGraphExec_t ex;
+    if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { use_graphs = false; return; }
+    capturing = true;
+    run(s);
+    capturing = false;
+    if (hipStreamEndCapture(stream, &g) != hipSuccess || hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) {
+      fprintf(stderr, "[laya] graph capture failed; continuing without graphs\n");
+      (void)hipGetLastError();
+      use_graphs = false;
+      return;
+    }
+    LAYA_HIP(hipGraphDestroy(g));
+    graphs[s] = ex;
+  }
+
+  int forward_batch(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
+                    float* logits, float* act) override {
+    std::vector<PassPlan> passes;
+    if (plan_passes(B, lens, ids, nmark, markers, qtypes, lim, &passes) != 0) return -1;
+    std::vector<int64_t> moff(B + 1, 0);
+    for (int b = 0; b < B; b++) moff[b + 1] = moff[b] + nmark[b];
+    for (const PassPlan& p : passes) {
+      stage_inputs(p);
+      Shape s{p.T, p.B, p.KT, p.R, p.VT, (int)p.tiles.size(), (int)p.gtiles.size()};
+      execute(s);
+      for (int i = 0; i < p.B; i++) {
+        const int b = p.first + i;
+        memcpy(logits + moff[b], h_logits + p.moff[i], (size_t)nmark[b] * 4);
+        memcpy(act + (size_t)b * cfg.n_act, h_act + (size_t)i * cfg.n_act, (size_t)cfg.n_act * 4);
+      }
+    }
+    return 0;
+  }
+
+  int replay(int iters, float* ms) override {
+    if (!have_last || iters < 1) return -1;
+    hipEvent_t a, b;
+    LAYA_HIP(hipEventCreate(&a));
+    LAYA_HIP(hipEventCreate(&b));
+    auto it = graphs.find(last);
+    const bool g = use_graphs && !prof.on && !dump_dir && it != graphs.end();
+    LAYA_HIP(hipEventRecord(a, stream));
+    for (int i = 0; i < iters; i++) {
+      if (g) LAYA_HIP(hipGraphLaunch(it->second, stream));
+      else run(last);
+    }
+    LAYA_HIP(hipEventRecord(b, stream));
+    LAYA_HIP(hipEventSynchronize(b));
+    LAYA_HIP(hipEventElapsedTime(ms, a, b));
+    LAYA_HIP(hipEventDestroy(a));
+    LAYA_HIP(hipEventDestroy(b));
+    return 0;
+  }
+
+  void warmup() override {
+    std::vector<int> ids(std::min(cfg.max_len, 64), cfg.cls_id), mk = {0};
+    int len = (int)ids.size(), nm = 1, qt = 0;
+    std::vector<float> lo(1), ac(cfg.n_act);
+    forward_batch(1, &len, ids.data(), &nm, mk.data(), &qt, lo.data(), ac.data());
+  }
+};
+
+}  // namespace laya
+
+// ---------------------------------------------------------------- C ABI
+using laya::EngineIface;
+static EngineIface* E(void* h) { return static_cast<EngineIface*>(h); }
+
+extern "C" {
+void* laya_create(const char* dir) {
+  const char* p = getenv("LAYA_PRECISION");
+  const std::string prec = p ? p : "bf16";
+  EngineIface* e = nullptr;
+  if (prec == "fp32") { auto* x = new laya::Engine<float>(); x->load(dir); e = x; }
+  else if (prec == "bf16") { auto* x = new laya::Engine<laya::bf16_t>(); x->load(dir); e = x; }
+  else { fprintf(stderr, "[laya] LAYA_PRECISION must be bf16 or fp32\n"); exit(1); }
+  return e;
+}
+int laya_forward_batch(void* h, int B, const int* lens, const int* ids, const int* nmark, const int* markers,
+                       const int* qtypes, float* logits, float* act) {
+  return E(h)->forward_batch(B, lens, ids, nmark, markers, qtypes, logits, act);
+}
+void laya_forward(void* h, const int* ids, int S, int valid_len, const int* markers, int K, int qtype, float* logits,
+                  float* act) {
+  (void)S;
+  E(h)->forward_batch(1, &valid_len, ids, &K, markers, &qtype, logits, act);
+}
+int laya_n_act(void* h) { return E(h)->cfg.n_act; }
+int laya_max_len(void* h) { return E(h)->cfg.max_len; }
+int laya_max_markers(void* h) { (void)h; return laya::kMaxMarkers; }
+float laya_temperature(void* h, int qtype) {
+  const auto& t = E(h)->cfg.temperature;
+  return qtype >= 0 && qtype < (int)t.size() ? t[qtype] : 1.0f;
+}
+void laya_prof_report(void* h, int iters) { E(h)->prof.report(iters); }
+void laya_prof_reset(void* h) { E(h)->prof.acc.clear(); }
+void laya_tune_all(void* h) { E(h)->warmup(); }
+
+int laya_ext_prof_enable(void* h, int on) { int was = E(h)->prof.on; E(h)->prof.on = on != 0; return was; }
+int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, long long* calls) {
+  auto& acc = E(h)->prof.acc;
+  if (i < 0 || i >= (int)acc.size()) return -1;
+  if (name && name_len > 0) { strncpy(name, std::get<0>(acc[i]).c_str(), name_len - 1); name[name_len - 1] = 0; }
+  if (ms) *ms = std::get<1>(acc[i]);
+  if (calls) *calls = std::get<2>(acc[i]);
+  return 0;
+}
+int laya_ext_replay(void* h, int iters, float* ms) { return E(h)->replay(iters, ms); }
+int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
+                  int K, void* stream, int iters, float* ms) {
+  using namespace laya;
+  if ((dtype != 0 && dtype != 1) || (epi != 0 && epi != 1) || iters < 1) return -1;
+  GemmArgs g;
+  g.A = A; g.lda = K; g.W = W; g.ldw = K; g.M = M; g.N = N; g.K = K; g.bias = bias; g.act = act;
+  if (epi == 0) { g.C = C; g.ldc = N; } else { g.X = (float*)C; g.ldx = N; }
+  const char* why = "";
+  if (!gemm_shape_ok(epi == 0 ? EPI_STORE : EPI_RESID, g, dtype == 0 ? 4 : 2, &why)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  hipEvent_t a, b;
+  if (ms) { LAYA_HIP(hipEventCreate(&a)); LAYA_HIP(hipEventCreate(&b)); LAYA_HIP(hipEventRecord(a, st)); }
+  for (int i = 0; i < iters; i++) {
+    if (dtype == 0) launch_gemm<float>(epi == 0 ? EPI_STORE : EPI_RESID, g, st);
+    else launch_gemm<bf16_t>(epi == 0 ? EPI_STORE : EPI_RESID, g, st);
+  }
+  if (ms) {
+    LAYA_HIP(hipEventRecord(b, st));
+    LAYA_HIP(hipEventSynchronize(b));
+    LAYA_HIP(hipEventElapsedTime(ms, a, b));
+    LAYA_HIP(hipEventDestroy(a)); LAYA_HIP(hipEventDestroy(b));
+  }
+  LAYA_HIP(hipGetLastError());
+  return 0;
+}
+const char* laya_ext_precision(void* h) { return E(h)->precision(); }
+}

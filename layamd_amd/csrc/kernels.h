@@ -1,0 +1,67 @@
+// Launchers of the gfx950 kernels.  T is the GEMM/attention storage type: float (fp32 path) or
+// bf16_t (bf16 path).  The residual stream is always fp32; 1-D parameters (LayerNorm weights and
+// biases, linear biases, type embedding) and the act head are always fp32.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "pack.h"
+
+namespace laya {
+
+// ---- LayerNorm family (one wave64 per row) ----
+// y = LN(src[row]) * w (+ b) (+ addtab[qt[seq[row]]]); src row = gather ? gather[row] : row.
+// Writes y32 (fp32, may alias x) and/or yT (storage type).  D % 4 == 0, D <= 2048.
+template <typename Tin, typename T>
+void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
+                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st);
+
+// xg[r] = x[rows[r]] (fp32 rows of width D)
+void launch_gather_rows(const float* x, const int* rows, float* xg, int R, int D, hipStream_t st);
+
+// ---- MFMA GEMM: C = A[M,K] . W[N,K]^T with a fused epilogue ----
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GEGLU = 3 };
+enum GemmAct { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+
+struct GemmArgs {
+  const void* A = nullptr; int lda = 0;          // [M][lda] T
+  const void* W = nullptr; int ldw = 0;          // [N][ldw] T ([out,in] weight)
+  int M = 0, N = 0, K = 0;
+  const float* bias = nullptr;                   // [N] in stored column order, or null
+  int act = ACT_NONE;                            // EPI_STORE only
+  void* C = nullptr; int ldc = 0;                // EPI_STORE: [M][ldc] T; EPI_GEGLU: [M][ldc] T, N/2 wide
+  float* X = nullptr; int ldx = 0;               // EPI_RESID: X[M][ldx] += result
+  // EPI_QKV: columns [q | k | v], each H*HD wide; q and k get RoPE when rope_cos != null (the
+  // weight rows of q and k are then stored in rope-pair order, see engine.hip)
+  void* Q = nullptr; void* Kt = nullptr; int ldqk = 0;
+  void* Vt = nullptr; int ldv = 0;               // V^T [H*HD][ldv]
+  int H = 0, HD = 0;
+  const int* pos = nullptr; const int* vcol = nullptr;
+  const float* rope_cos = nullptr; const float* rope_sin = nullptr;  // [max_len][HD/2]
+};
+
+template <typename T>
+void launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
+bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
+
+// ---- attention over packed sequences ----
+// Query tiles from `tiles`; gathered mode when gq != null (queries are gathered rows
+// grow[gq[tile.q0 + r]], outputs go to row gq[...] of O).  window_half = 0: all keys of the
+// sequence; otherwise keys with |i - j| <= window_half.
+template <typename T>
+void launch_attention(const T* Q, const T* K, int ldqk, const T* Vt, int ldv, T* O, int ldo, const AttnTile* tiles,
+                      int ntiles, int H, const int* soff, const int* vlen, const int* vbase, const int* gq,
+                      const int* grow, int window_half, float scale, hipStream_t st);
+
+// ---- scorer tail and act head ----
+// logits[r] = dot(h[r], w) + b[0]   (fp32 accumulate)
+template <typename T>
+void launch_row_dot(const T* h, int ldh, const float* w, const float* b, float* logits, int R, int D, hipStream_t st);
+
+// act head per question (ref/rl_common.py:116-123): softmax over its logits -> features
+// [top1, top1-top2, H(p)/ln(max(k,2)), max(k,2)/255] ++ cls row -> GELU(W0 . + b0) -> W2 . + b2
+void launch_act_head(const float* cls, int D, const float* logits, const int* moff, const int* nmark,
+                     const float* W0, const float* B0, const float* W2, const float* B2, int n_act, float* out, int B,
+                     hipStream_t st);
+
+}  // namespace laya

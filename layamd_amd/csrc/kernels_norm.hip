@@ -1,0 +1,189 @@
+// LayerNorm family, gathers, and the decision head's small kernels for gfx950.
+//
+// LayerNorm is HBM-bound: one wave64 owns one row, keeps it in registers (D/256 float4 per
+// lane), reduces mean and variance with wave shuffles (no LDS, no barriers), and writes the
+// normalised row in one pass.  Four rows per 256-thread workgroup.
+#include "kernels.h"
+
+namespace laya {
+
+static constexpr int kLnMaxChunks = 8;     // D <= 8 * 64 * 4 = 2048
+
+template <typename Tin> struct Ld4;
+template <> struct Ld4<float> {
+  static __device__ __forceinline__ float4 at(const float* p, int c) { return reinterpret_cast<const float4*>(p)[c]; }
+};
+template <> struct Ld4<bf16_t> {
+  static __device__ __forceinline__ float4 at(const bf16_t* p, int c) {
+    uint2 u = reinterpret_cast<const uint2*>(p)[c];
+    return make_float4(bf2f(u.x & 0xFFFF), bf2f(u.x >> 16), bf2f(u.y & 0xFFFF), bf2f(u.y >> 16));
+  }
+};
+template <typename T> struct St4;
+template <> struct St4<float> {
+  static __device__ __forceinline__ void at(float* p, int c, float4 v) { reinterpret_cast<float4*>(p)[c] = v; }
+};
+template <> struct St4<bf16_t> {
+  static __device__ __forceinline__ void at(bf16_t* p, int c, float4 v) {
+    uint2 u;
+    u.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
+    u.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+    reinterpret_cast<uint2*>(p)[c] = u;
+  }
+};
+
+template <typename Tin, typename T>
+__global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows,
+                                                   int D, float eps, const float* __restrict__ w,
+                                                   const float* __restrict__ b, const float* __restrict__ addtab,
+                                                   const int* __restrict__ qt, const int* __restrict__ seq, float* y32,  // may alias x
+                                                   T* __restrict__ yT) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nc = D >> 2;
+  const size_t src = gather ? (size_t)gather[row] : (size_t)row;
+  const Tin* xr = x + src * D;
+  float4 v[kLnMaxChunks];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kLnMaxChunks; j++) {
+    const int c = lane + 64 * j;
+    if (c < nc) { v[j] = Ld4<Tin>::at(xr, c); s += (v[j].x + v[j].y) + (v[j].z + v[j].w); }
+  }
+  const float mean = wave_sum(s) / D;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < kLnMaxChunks; j++) {
+    const int c = lane + 64 * j;
+    if (c < nc) {
+      const float a = v[j].x - mean, bb = v[j].y - mean, cc = v[j].z - mean, d = v[j].w - mean;
+      q += (a * a + bb * bb) + (cc * cc + d * d);
+    }
+  }
+  const float inv = rsqrtf(wave_sum(q) / D + eps);
+  const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
+#pragma unroll
+  for (int j = 0; j < kLnMaxChunks; j++) {
+    const int c = lane + 64 * j;
+    if (c < nc) {
+      const float4 ww = reinterpret_cast<const float4*>(w)[c];
+      float4 o = make_float4((v[j].x - mean) * inv * ww.x, (v[j].y - mean) * inv * ww.y,
+                             (v[j].z - mean) * inv * ww.z, (v[j].w - mean) * inv * ww.w);
+      if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
+      if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
+      if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
+      if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
+    }
+  }
+}
+
+template <typename Tin, typename T>
+void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
+                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st) {
+  if (D % 4 || D > kLnMaxChunks * 256) { fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D); exit(1); }
+  if (rows <= 0) return;
+  hipLaunchKernelGGL((k_layernorm<Tin, T>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
+                     addtab, qt, seq, y32, yT);
+}
+
+template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
+                                             const float*, const int*, const int*, float*, float*, hipStream_t);
+template void launch_layernorm<float, bf16_t>(const float*, const int*, int, int, float, const float*, const float*,
+                                              const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
+template void launch_layernorm<bf16_t, bf16_t>(const bf16_t*, const int*, int, int, float, const float*, const float*,
+                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
+
+__global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, const int* __restrict__ rows,
+                                                     float* __restrict__ xg, int R, int D) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const float4* s = reinterpret_cast<const float4*>(x + (size_t)rows[r] * D);
+  float4* d = reinterpret_cast<float4*>(xg + (size_t)r * D);
+  for (int c = lane; c < D / 4; c += 64) d[c] = s[c];
+}
+
+void launch_gather_rows(const float* x, const int* rows, float* xg, int R, int D, hipStream_t st) {
+  if (R <= 0) return;
+  hipLaunchKernelGGL(k_gather_rows, dim3((R + 3) / 4), dim3(256), 0, st, x, rows, xg, R, D);
+}
+
+// ---- scorer tail: one wave per row, fp32 accumulation ----
+template <typename T>
+__global__ __launch_bounds__(256) void k_row_dot(const T* __restrict__ h, int ldh, const float* __restrict__ w,
+                                                 const float* __restrict__ b, float* __restrict__ logits, int R, int D) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const T* hr = h + (size_t)r * ldh;
+  float s = 0.f;
+  for (int c = lane; c < D; c += 64) s += Elt<T>::ld(hr + c) * w[c];
+  s = wave_sum(s);
+  if (lane == 0) logits[r] = s + b[0];
+}
+
+template <typename T>
+void launch_row_dot(const T* h, int ldh, const float* w, const float* b, float* logits, int R, int D, hipStream_t st) {
+  if (R <= 0) return;
+  hipLaunchKernelGGL((k_row_dot<T>), dim3((R + 3) / 4), dim3(256), 0, st, h, ldh, w, b, logits, R, D);
+}
+template void launch_row_dot<float>(const float*, int, const float*, const float*, float*, int, int, hipStream_t);
+template void launch_row_dot<bf16_t>(const bf16_t*, int, const float*, const float*, float*, int, int, hipStream_t);
+
+// ---- act head: one 256-thread workgroup per question ----
+// Follows ref/rl_common.py:116-123: p = softmax(logits over the question's markers); k =
+// max(nmark, 2); features [top1, top1 - top2, -sum p log(max(p, 1e-9)) / ln k, k / 255];
+// hidden = GELU(W0 [cls, features] + b0) with W0 [256][D + 4]; out = W2 hidden + b2.
+__global__ __launch_bounds__(256) void k_act_head(const float* __restrict__ cls, int D, const float* __restrict__ logits,
+                                                  const int* __restrict__ moff, const int* __restrict__ nmark,
+                                                  const float* __restrict__ W0, const float* __restrict__ B0,
+                                                  const float* __restrict__ W2, const float* __restrict__ B2, int n_act,
+                                                  float* __restrict__ out) {
+  extern __shared__ float sm[];
+  float* in = sm;               // D + 4
+  float* hid = sm + D + 4;      // 256
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  for (int d = t; d < D; d += 256) in[d] = cls[(size_t)b * D + d];
+  if (t == 0) {
+    const float* z = logits + moff[b];
+    const int K = nmark[b];
+    float mx = -INFINITY;
+    for (int i = 0; i < K; i++) mx = fmaxf(mx, z[i]);
+    float s = 0.f;
+    for (int i = 0; i < K; i++) s += expf(z[i] - mx);
+    float t1 = 0.f, t2 = 0.f, ent = 0.f;
+    for (int i = 0; i < K; i++) {
+      const float p = expf(z[i] - mx) / s;
+      ent -= p * logf(fmaxf(p, 1e-9f));
+      if (p > t1) { t2 = t1; t1 = p; } else if (p > t2) t2 = p;
+    }
+    const float k = (float)(K < 2 ? 2 : K);
+    in[D] = t1; in[D + 1] = t1 - t2; in[D + 2] = ent / logf(k); in[D + 3] = k / 255.f;
+  }
+  __syncthreads();
+  for (int j = wv; j < 256; j += 4) {
+    const float* wr = W0 + (size_t)j * (D + 4);
+    float a = 0.f;
+    for (int i = lane; i < D + 4; i += 64) a += wr[i] * in[i];
+    a = wave_sum(a);
+    if (lane == 0) hid[j] = gelu_erf(a + B0[j]);
+  }
+  __syncthreads();
+  for (int j = wv; j < n_act; j += 4) {
+    const float* wr = W2 + (size_t)j * 256;
+    float a = 0.f;
+    for (int i = lane; i < 256; i += 64) a += wr[i] * hid[i];
+    a = wave_sum(a);
+    if (lane == 0) out[(size_t)b * n_act + j] = a + B2[j];
+  }
+}
+
+void launch_act_head(const float* cls, int D, const float* logits, const int* moff, const int* nmark, const float* W0,
+                     const float* B0, const float* W2, const float* B2, int n_act, float* out, int B, hipStream_t st) {
+  if (B <= 0) return;
+  hipLaunchKernelGGL(k_act_head, dim3(B), dim3(256), (D + 4 + 256) * sizeof(float), st, cls, D, logits, moff, nmark, W0,
+                     B0, W2, B2, n_act, out);
+}
+
+}  // namespace laya

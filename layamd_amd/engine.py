@@ -1,0 +1,206 @@
+"""ctypes binding of liblaya.so, shaped like the reference server's binding.
+
+`Engine(lib_path, model_dir)` and `Engine.forward_batch(seqs, markers, qtypes)` have the same
+names, arguments, return values and error behaviour as the reference's server-side class
+(server/laya_server.py:18-50): one `laya_forward_batch` call per request batch, ValueError when
+the engine rejects the batch, per-question logits arrays plus an [B, n_act] act array.  The
+`forward_flat` variant takes the ABI's flat arrays directly (numpy), and the `laya_ext_*`
+measurement hooks are exposed for the benchmark.
+
+The library is the in-tree build (layamd_amd/liblaya.so, or $LAYA_LIB).  There is no fallback:
+a missing library raises.
+"""
+import ctypes
+import itertools
+import os
+from array import array
+from typing import List, Optional
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_LIB = os.path.join(PKG, "liblaya.so")
+HOST_LIB = os.path.join(PKG, "liblaya_host.so")
+
+ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act", "laya_max_len",
+               "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
+EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm"]
+
+_IP = ctypes.POINTER(ctypes.c_int)
+_FP = ctypes.POINTER(ctypes.c_float)
+
+
+def lib_path() -> str:
+    return os.environ.get("LAYA_LIB", DEFAULT_LIB)
+
+
+def load_library(path: Optional[str] = None) -> ctypes.CDLL:
+    """Loads liblaya.so and declares every exported signature (no GPU work happens here)."""
+    path = path or lib_path()
+    if not os.path.exists(path):
+        raise FileNotFoundError("liblaya.so not built at %s (run python -m layamd_amd.build)" % path)
+    L = ctypes.CDLL(path)
+    L.laya_create.restype = ctypes.c_void_p
+    L.laya_create.argtypes = [ctypes.c_char_p]
+    L.laya_forward_batch.restype = ctypes.c_int
+    L.laya_forward_batch.argtypes = [ctypes.c_void_p, ctypes.c_int, _IP, _IP, _IP, _IP, _IP, _FP, _FP]
+    L.laya_forward.restype = None
+    L.laya_forward.argtypes = [ctypes.c_void_p, _IP, ctypes.c_int, ctypes.c_int, _IP, ctypes.c_int, ctypes.c_int, _FP, _FP]
+    for f in ("laya_n_act", "laya_max_len", "laya_max_markers"):
+        getattr(L, f).argtypes = [ctypes.c_void_p]
+        getattr(L, f).restype = ctypes.c_int
+    L.laya_temperature.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    L.laya_temperature.restype = ctypes.c_float
+    L.laya_prof_report.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    L.laya_prof_report.restype = None
+    L.laya_prof_reset.argtypes = [ctypes.c_void_p]
+    L.laya_prof_reset.restype = None
+    L.laya_tune_all.argtypes = [ctypes.c_void_p]
+    L.laya_tune_all.restype = None
+    L.laya_ext_prof_enable.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    L.laya_ext_prof_enable.restype = ctypes.c_int
+    L.laya_ext_prof_stage.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_longlong)]
+    L.laya_ext_prof_stage.restype = ctypes.c_int
+    L.laya_ext_replay.argtypes = [ctypes.c_void_p, ctypes.c_int, _FP]
+    L.laya_ext_replay.restype = ctypes.c_int
+    L.laya_ext_precision.argtypes = [ctypes.c_void_p]
+    L.laya_ext_precision.restype = ctypes.c_char_p
+    L.laya_ext_gemm.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.c_void_p, ctypes.c_int, _FP]
+    L.laya_ext_gemm.restype = ctypes.c_int
+    return L
+
+
+def gemm(lib, A, W, C, bias=None, act=0, residual=False, stream=None, iters=1):
+    """Runs the engine GEMM on torch device tensors (A [M,K], W [N,K], C [M,N]); returns total ms."""
+    import torch
+    dtype = 1 if A.dtype == torch.bfloat16 else 0
+    ms = ctypes.c_float()
+    st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    rc = lib.laya_ext_gemm(dtype, 1 if residual else 0, A.data_ptr(), W.data_ptr(), C.data_ptr(),
+                           bias.data_ptr() if bias is not None else None, act, A.shape[0], W.shape[0], A.shape[1],
+                           ctypes.c_void_p(st), iters, ctypes.byref(ms))
+    if rc != 0:
+        raise ValueError("gemm shape rejected: M=%d N=%d K=%d" % (A.shape[0], W.shape[0], A.shape[1]))
+    return ms.value
+
+
+def _ptr(a: np.ndarray, ct):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+class Engine:
+    """One engine handle (not thread-safe; the engine lives until the process exits)."""
+
+    def __init__(self, lib_path_: Optional[str], model_dir: str, precision: Optional[str] = None, env=None):
+        if precision is not None:
+            os.environ["LAYA_PRECISION"] = precision
+        for k, v in (env or {}).items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = str(v)
+        self.lib = L = load_library(lib_path_)
+        self.h = L.laya_create(model_dir.encode())
+        if not self.h:
+            raise RuntimeError("laya_create failed for %s" % model_dir)
+        self.n_act = L.laya_n_act(self.h)
+        self.max_markers = L.laya_max_markers(self.h)
+        self.max_len = L.laya_max_len(self.h)
+        self.precision = L.laya_ext_precision(self.h).decode()
+
+    # --- the reference server's call shape (server/laya_server.py:33-50)
+    def forward_batch(self, seqs: List[List[int]], markers: List[List[int]], qtypes: List[int]):
+        B = len(seqs)
+        lens = array("i", (len(s) for s in seqs))
+        nm = array("i", (len(m) for m in markers))
+        ids = array("i", itertools.chain.from_iterable(seqs))
+        mk = array("i", itertools.chain.from_iterable(markers))
+        qt = array("i", qtypes)
+        buf = lambda a: (ctypes.c_int * len(a)).from_buffer(a) if len(a) else (ctypes.c_int * 1)()
+        lo = (ctypes.c_float * max(1, len(mk)))()
+        ac = (ctypes.c_float * max(1, B * self.n_act))()
+        if self.lib.laya_forward_batch(self.h, B, buf(lens), buf(ids), buf(nm), buf(mk), buf(qt), lo, ac) != 0:
+            raise ValueError("engine rejected batch (sequence too long or too many options)")
+        lo = np.ctypeslib.as_array(lo)[:len(mk)]
+        ac = np.ctypeslib.as_array(ac)[:B * self.n_act].reshape(B, self.n_act)
+        out, off = [], 0
+        for m in markers:
+            out.append(lo[off:off + len(m)].copy())
+            off += len(m)
+        return out, ac.copy()
+
+    # --- flat numpy arrays, exactly the ABI's arguments
+    def forward_flat(self, lens, ids, nmark, markers, qtypes):
+        lens = np.ascontiguousarray(lens, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        nmark = np.ascontiguousarray(nmark, np.int32)
+        markers = np.ascontiguousarray(markers, np.int32)
+        qtypes = np.ascontiguousarray(qtypes, np.int32)
+        B = len(lens)
+        logits = np.zeros(max(1, int(nmark.sum()) if B else 0), np.float32)
+        act = np.zeros(max(1, B * self.n_act), np.float32)
+        rc = self.lib.laya_forward_batch(self.h, B, _ptr(lens, ctypes.c_int), _ptr(ids, ctypes.c_int),
+                                         _ptr(nmark, ctypes.c_int), _ptr(markers, ctypes.c_int),
+                                         _ptr(qtypes, ctypes.c_int), _ptr(logits, ctypes.c_float),
+                                         _ptr(act, ctypes.c_float))
+        if rc != 0:
+            raise ValueError("engine rejected batch (sequence too long or too many options)")
+        return logits[:int(nmark.sum())], act[:B * self.n_act].reshape(B, self.n_act)
+
+    def forward_rc(self, lens, ids, nmark, markers, qtypes) -> int:
+        """Raw return code of laya_forward_batch (for validation tests)."""
+        lens = np.ascontiguousarray(lens, np.int32)
+        ids = np.ascontiguousarray(ids if len(ids) else [0], np.int32)
+        nmark = np.ascontiguousarray(nmark, np.int32)
+        markers = np.ascontiguousarray(markers if len(markers) else [0], np.int32)
+        qtypes = np.ascontiguousarray(qtypes, np.int32)
+        logits = np.zeros(max(1, int(np.maximum(nmark, 0).sum())), np.float32)
+        act = np.zeros(max(1, len(lens) * self.n_act), np.float32)
+        return self.lib.laya_forward_batch(self.h, len(lens), _ptr(lens, ctypes.c_int), _ptr(ids, ctypes.c_int),
+                                           _ptr(nmark, ctypes.c_int), _ptr(markers, ctypes.c_int),
+                                           _ptr(qtypes, ctypes.c_int), _ptr(logits, ctypes.c_float),
+                                           _ptr(act, ctypes.c_float))
+
+    def forward_one(self, ids, markers, qtype: int):
+        """laya_forward (single question)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        markers = np.ascontiguousarray(markers, np.int32)
+        logits = np.zeros(len(markers), np.float32)
+        act = np.zeros(self.n_act, np.float32)
+        self.lib.laya_forward(self.h, _ptr(ids, ctypes.c_int), len(ids), len(ids), _ptr(markers, ctypes.c_int),
+                              len(markers), int(qtype), _ptr(logits, ctypes.c_float), _ptr(act, ctypes.c_float))
+        return logits, act
+
+    def temperature(self, qtype: int) -> float:
+        return float(self.lib.laya_temperature(self.h, qtype))
+
+    def tune_all(self):
+        self.lib.laya_tune_all(self.h)
+
+    # --- measurement hooks
+    def prof_enable(self, on: bool) -> bool:
+        return bool(self.lib.laya_ext_prof_enable(self.h, 1 if on else 0))
+
+    def prof_reset(self):
+        self.lib.laya_prof_reset(self.h)
+
+    def prof_report(self, iters: int = 1):
+        self.lib.laya_prof_report(self.h, iters)
+
+    def prof_stages(self):
+        out, i = {}, 0
+        name = ctypes.create_string_buffer(64)
+        ms, calls = ctypes.c_double(), ctypes.c_longlong()
+        while self.lib.laya_ext_prof_stage(self.h, i, name, 64, ctypes.byref(ms), ctypes.byref(calls)) == 0:
+            out[name.value.decode()] = (ms.value, calls.value)
+            i += 1
+        return out
+
+    def replay(self, iters: int) -> float:
+        ms = ctypes.c_float()
+        if self.lib.laya_ext_replay(self.h, iters, ctypes.byref(ms)) != 0:
+            raise RuntimeError("no pass to replay")
+        return ms.value

