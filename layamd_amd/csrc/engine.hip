@@ -112,20 +112,20 @@ struct Engine : EngineIface {
   float *cos_g, *sin_g, *cos_l, *sin_l;
 
   // activations
-  int64_t MT = 0, RG = 0, VTC = 0;
-  float *x = nullptr, *xg = nullptr, *d_logits = nullptr, *d_act = nullptr;
+  int64_t MT = 0, RG = 0, VTC = 0;   // rows, gathered rows, V^T columns (rows + one key block)
+  float *x = nullptr, *xg = nullptr, *d_logits = nullptr, *d_act = nullptr, *d_act_hidden = nullptr;
   T *xn, *q, *k, *vt, *ao, *mg, *ff, *aog, *xng, *sh;
 
   // per-pass index arrays: device + pinned host mirrors at fixed addresses (graph replay)
-  int *d_ids, *d_pos, *d_seq, *d_vcol, *d_soff, *d_vlen, *d_vbase, *d_qt, *d_nm, *d_moff, *d_gq, *d_grow;
-  int *h_ids, *h_pos, *h_seq, *h_vcol, *h_soff, *h_vlen, *h_vbase, *h_qt, *h_nm, *h_moff, *h_gq, *h_grow;
+  int *d_ids, *d_pos, *d_seq, *d_soff, *d_vlen, *d_qt, *d_nm, *d_moff, *d_gq, *d_grow;
+  int *h_ids, *h_pos, *h_seq, *h_soff, *h_vlen, *h_qt, *h_nm, *h_moff, *h_gq, *h_grow;
   AttnTile *d_tiles, *d_gtiles, *h_tiles, *h_gtiles;
   float *h_logits, *h_act;
 
   struct Shape {
-    int rows, B, KT, R, VT, nt, ngt;
+    int rows, B, KT, R, nt, ngt;
     bool operator<(const Shape& o) const {
-      return std::tie(rows, B, KT, R, VT, nt, ngt) < std::tie(o.rows, o.B, o.KT, o.R, o.VT, o.nt, o.ngt);
+      return std::tie(rows, B, KT, R, nt, ngt) < std::tie(o.rows, o.B, o.KT, o.R, o.nt, o.ngt);
     }
   };
   std::map<Shape, hipGraphExec_t> graphs;
@@ -194,26 +194,13 @@ struct Engine : EngineIface {
     LAYA_HIP(hipMemcpy(d, o.data(), o.size() * sizeof(T), hipMemcpyHostToDevice));
     return d;
   }
-  // q and k rows of each head reordered d = [0..15, 32..47, 16..31, 48..63] (RoPE pairs adjacent)
-  std::vector<int> rope_perm() const {
-    const int D = cfg.d, HD = cfg.head_dim;
-    std::vector<int> p(3 * D);
-    for (int r = 0; r < 3 * D; r++) {
-      const int sec = r / D, e = r % D, h = e / HD, t = e % HD;
-      if (sec == 2) { p[r] = r; continue; }
-      const int blk = t / 16, off = t % 16;
-      const int d = blk == 0 ? off : blk == 1 ? 32 + off : blk == 2 ? 16 + off : 48 + off;
-      p[r] = sec * D + h * HD + d;
-    }
-    return p;
-  }
-  // Wi rows as alternating 16-row blocks of input rows and gate rows
+  // Wi rows as alternating 32-row blocks of input rows and gate rows (GeGLU epilogue pairs)
   std::vector<int> geglu_perm() const {
     const int I = cfg.intermediate;
     std::vector<int> p(2 * I);
     for (int r = 0; r < 2 * I; r++) {
-      const int pair = r / 32, within = r % 32;
-      p[r] = within < 16 ? pair * 16 + within : I + pair * 16 + (within - 16);
+      const int pair = r / 64, within = r % 64;
+      p[r] = within < 32 ? pair * 32 + within : I + pair * 32 + (within - 32);
     }
     return p;
   }
@@ -228,8 +215,8 @@ struct Engine : EngineIface {
     verbose = getenv("LAYA_VERBOSE") != nullptr;
     printf("%s[laya] precision=%s (gfx950 MFMA path)\n", cfg.describe().c_str(), precision());
     const int D = cfg.d, I = cfg.intermediate, FF = cfg.head_ffn, H = cfg.n_heads, HD = cfg.head_dim, V = cfg.vocab;
-    if (HD != 64 || D % 64 || I % 16 || cfg.head_layers < 1 || cfg.n_act < 1 || cfg.n_act > 256) {
-      fprintf(stderr, "[laya] unsupported model shape (needs head_dim 64, d %% 64 == 0, intermediate %% 16 == 0, "
+    if (HD != 64 || D % 64 || I % 32 || cfg.head_layers < 1 || cfg.n_act < 1 || cfg.n_act > 256) {
+      fprintf(stderr, "[laya] unsupported model shape (needs head_dim 64, d %% 64 == 0, intermediate %% 32 == 0, "
                       "head_layers >= 1)\n");
       exit(1);
     }
@@ -240,12 +227,12 @@ struct Engine : EngineIface {
     emb_norm = up_f32(st, "encoder.embeddings.norm.weight", {D});
     final_norm = up_f32(st, "encoder.final_norm.weight", {D});
     type_emb = up_f32(st, "type_emb.weight", {3, D});
-    const std::vector<int> rp = rope_perm(), gp = geglu_perm();
+    const std::vector<int> gp = geglu_perm();
     enc.resize(cfg.n_layers);
     for (int i = 0; i < cfg.n_layers; i++) {
       const std::string p = "encoder.layers." + std::to_string(i) + ".";
       if (st.get(p + "attn_norm.weight") || i > 0) enc[i].attn_norm = up_f32(st, p + "attn_norm.weight", {D});
-      enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D, rp);
+      enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D);
       enc[i].Wo = up_mat(st, p + "attn.Wo.weight", D, D);
       enc[i].mlp_norm = up_f32(st, p + "mlp_norm.weight", {D});
       enc[i].Wi = up_mat(st, p + "mlp.Wi.weight", 2 * I, D, gp);
@@ -273,7 +260,7 @@ struct Engine : EngineIface {
     // RoPE tables [max_len][HD/2], as HF builds them (modeling_modernbert.py:136-163): fp32
     // inverse frequencies theta^(-2i/HD), fp32 position products, cos/sin of those.
     {
-      const int L = cfg.max_len, H2 = HD / 2;
+      const int L = cfg.max_len + kRowAlign, H2 = HD / 2;   // padding rows continue past max_len
       std::vector<float> cg((size_t)L * H2), sg(cg.size()), cl(cg.size()), sl(cg.size());
       for (int i = 0; i < H2; i++) {
         const float ig = 1.0f / powf(cfg.rope_theta_global, (float)(2 * i) / (float)HD);
@@ -295,12 +282,14 @@ struct Engine : EngineIface {
     // limits and buffers
     lim.max_len = cfg.max_len;
     lim.vocab = V;
+    lim.pad_id = cfg.pad_id;
+    if (cfg.pad_id < 0 || cfg.pad_id >= V) { fprintf(stderr, "[laya] pad_token_id outside the vocabulary\n"); exit(1); }
     lim.pass_tokens = std::max(env_int("LAYA_MAX_TOKENS", 65536), cfg.max_len);
     lim.pass_tokens = std::min(std::max(env_int("LAYA_PASS_TOKENS", lim.pass_tokens), cfg.max_len), lim.pass_tokens);
     lim.max_seqs = std::max(1, env_int("LAYA_MAX_SEQS", 512));
     lim.max_grows = std::max(env_int("LAYA_MAX_GATHERED", 32768), kMaxMarkers + 1);
     caps = pass_caps(lim);
-    MT = caps.rows; RG = caps.grows; VTC = (caps.vt_cols + 63) / 64 * 64;
+    MT = caps.rows; RG = caps.grows; VTC = (MT + 64 + 63) / 64 * 64;
     x = dalloc<float>((size_t)MT * D);
     xn = dalloc<T>((size_t)MT * D); q = dalloc<T>((size_t)MT * D); k = dalloc<T>((size_t)MT * D);
     ao = dalloc<T>((size_t)MT * D);
@@ -311,12 +300,13 @@ struct Engine : EngineIface {
     aog = dalloc<T>((size_t)RG * D); xng = dalloc<T>((size_t)RG * D); sh = dalloc<T>((size_t)RG * D);
     d_logits = dalloc<float>((size_t)RG);
     d_act = dalloc<float>((size_t)lim.max_seqs * cfg.n_act);
+    d_act_hidden = dalloc<float>((size_t)lim.max_seqs * 256);
     h_logits = halloc<float>((size_t)RG);
     h_act = halloc<float>((size_t)lim.max_seqs * cfg.n_act);
     auto pair = [&](int** d, int** h, size_t n) { *d = dalloc<int>(n); *h = halloc<int>(n); };
-    pair(&d_ids, &h_ids, MT); pair(&d_pos, &h_pos, MT); pair(&d_seq, &h_seq, MT); pair(&d_vcol, &h_vcol, MT);
+    pair(&d_ids, &h_ids, MT); pair(&d_pos, &h_pos, MT); pair(&d_seq, &h_seq, MT);
     pair(&d_soff, &h_soff, lim.max_seqs + 1); pair(&d_vlen, &h_vlen, lim.max_seqs);
-    pair(&d_vbase, &h_vbase, lim.max_seqs); pair(&d_qt, &h_qt, lim.max_seqs);
+    pair(&d_qt, &h_qt, lim.max_seqs);
     pair(&d_nm, &h_nm, lim.max_seqs); pair(&d_moff, &h_moff, lim.max_seqs);
     pair(&d_gq, &h_gq, RG); pair(&d_grow, &h_grow, RG);
     d_tiles = dalloc<AttnTile>(caps.tiles); h_tiles = halloc<AttnTile>(caps.tiles);
@@ -335,9 +325,9 @@ struct Engine : EngineIface {
   // ------------------------------------------------------------ one pass
   void stage_inputs(const PassPlan& p) {
     memcpy(h_ids, p.ids.data(), p.T * 4); memcpy(h_pos, p.pos.data(), p.T * 4);
-    memcpy(h_seq, p.seq.data(), p.T * 4); memcpy(h_vcol, p.vcol.data(), p.T * 4);
+    memcpy(h_seq, p.seq.data(), p.T * 4);
     memcpy(h_soff, p.soff.data(), (p.B + 1) * 4); memcpy(h_vlen, p.vlen.data(), p.B * 4);
-    memcpy(h_vbase, p.vbase.data(), p.B * 4); memcpy(h_qt, p.qt.data(), p.B * 4);
+    memcpy(h_qt, p.qt.data(), p.B * 4);
     memcpy(h_nm, p.nm.data(), p.B * 4); memcpy(h_moff, p.moff.data(), p.B * 4);
     memcpy(h_gq, p.gq.data(), p.gq.size() * 4); memcpy(h_grow, p.grow.data(), p.R * 4);
     memcpy(h_tiles, p.tiles.data(), p.tiles.size() * sizeof(AttnTile));
@@ -366,8 +356,8 @@ struct Engine : EngineIface {
     const int T_ = s.rows, B = s.B, KT = s.KT, R = s.R;
     hipStream_t st = stream;
     auto h2d = [&](void* d, const void* h, size_t n) { LAYA_HIP(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st)); };
-    h2d(d_ids, h_ids, T_ * 4); h2d(d_pos, h_pos, T_ * 4); h2d(d_seq, h_seq, T_ * 4); h2d(d_vcol, h_vcol, T_ * 4);
-    h2d(d_soff, h_soff, (B + 1) * 4); h2d(d_vlen, h_vlen, B * 4); h2d(d_vbase, h_vbase, B * 4);
+    h2d(d_ids, h_ids, T_ * 4); h2d(d_pos, h_pos, T_ * 4); h2d(d_seq, h_seq, T_ * 4);
+    h2d(d_soff, h_soff, (B + 1) * 4); h2d(d_vlen, h_vlen, B * 4);
     h2d(d_qt, h_qt, B * 4); h2d(d_nm, h_nm, B * 4); h2d(d_moff, h_moff, B * 4);
     h2d(d_gq, h_gq, R * 4); h2d(d_grow, h_grow, R * 4);
     h2d(d_tiles, h_tiles, s.nt * sizeof(AttnTile)); h2d(d_gtiles, h_gtiles, s.ngt * sizeof(AttnTile));
@@ -384,12 +374,12 @@ struct Engine : EngineIface {
                                                    nullptr, nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, e.Wqkv, T_, 3 * D, D, nullptr);
-        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos; g.vcol = d_vcol;
+        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
         g.rope_cos = glob ? cos_g : cos_l; g.rope_sin = glob ? sin_g : sin_l;
         STAGE("enc:gemm_qkv_rope", launch_gemm<T>(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
-            launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, d_vbase, nullptr,
+            launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, nullptr,
                                 nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
@@ -427,11 +417,11 @@ struct Engine : EngineIface {
                                                   nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, hl.inW, T_, 3 * D, D, hl.inB);
-        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos; g.vcol = d_vcol;
+        g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
         STAGE("head:gemm_qkv", launch_gemm<T>(EPI_QKV, g, st));
       }
       if (!last) {
-        STAGE("head:attn", launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, d_vbase,
+        STAGE("head:attn", launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen,
                                                nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
@@ -445,7 +435,7 @@ struct Engine : EngineIface {
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
         STAGE("head:attn_gathered", launch_attention<T>(q, k, D, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
-                                                        d_vlen, d_vbase, d_gq, d_grow, 0, scale, st));
+                                                        d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
         { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D;
           STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
@@ -465,7 +455,7 @@ struct Engine : EngineIface {
       STAGE("scorer:gemm_gelu", launch_gemm<T>(EPI_STORE, g, st)); }
     STAGE("scorer:dot", launch_row_dot<T>(sh, D, sc3w, sc3b, d_logits, KT, D, st));
     STAGE("act_head", launch_act_head(xg + (size_t)KT * D, D, d_logits, d_moff, d_nm, ah0W, ah0b, ah2W, ah2b,
-                                      cfg.n_act, d_act, B, st));
+                                      cfg.n_act, d_act, d_act_hidden, B, st));
 #undef STAGE
     LAYA_HIP(hipMemcpyAsync(h_logits, d_logits, (size_t)KT * 4, hipMemcpyDeviceToHost, st));
     LAYA_HIP(hipMemcpyAsync(h_act, d_act, (size_t)B * cfg.n_act * 4, hipMemcpyDeviceToHost, st));
@@ -510,7 +500,7 @@ struct Engine : EngineIface {
     for (int b = 0; b < B; b++) moff[b + 1] = moff[b] + nmark[b];
     for (const PassPlan& p : passes) {
       stage_inputs(p);
-      Shape s{p.T, p.B, p.KT, p.R, p.VT, (int)p.tiles.size(), (int)p.gtiles.size()};
+      Shape s{p.T, p.B, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size()};
       execute(s);
       for (int i = 0; i < p.B; i++) {
         const int b = p.first + i;

@@ -13,32 +13,32 @@ extern "C" {
 
 // Plans a laya_forward_batch call.  Returns -1 on invalid input, else the number of passes.
 // For pass `which` it fills (when the pointers are non-null and large enough):
-//   dims[10] = first, B, T, VT, KT, R, ntiles, ngtiles, len(gq), 0
-//   rows[4*T] = ids | pos | seq | vcol; seqs[6*B+1] = soff(B+1) | vlen | vbase | qt | nm | moff
+//   dims[10] = first, B, T, valid, KT, R, ntiles, ngtiles, len(gq), 0
+//   rows[3*T] = ids | pos | seq; seqs[5*B+1] = soff(B+1) | vlen | qt | nm | moff
 //   tiles[4*ntiles], gtiles[4*ngtiles], gq[len], grow[R]
 int laya_host_plan(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
-                   int max_len, int pass_tokens, int max_seqs, int max_grows, int vocab, int which, int* dims,
+                   int max_len, int pass_tokens, int max_seqs, int max_grows, int vocab, int pad_id, int which, int* dims,
                    int* rows, int* seqs, int* tiles, int* gtiles, int* gq, int* grow) {
   PackLimits lim;
   lim.max_len = max_len; lim.pass_tokens = pass_tokens; lim.max_seqs = max_seqs; lim.max_grows = max_grows;
   lim.vocab = vocab;
+  lim.pad_id = pad_id;
   std::vector<PassPlan> ps;
   if (plan_passes(B, lens, ids, nmark, markers, qtypes, lim, &ps) != 0) return -1;
   if (which >= 0 && which < (int)ps.size()) {
     const PassPlan& p = ps[which];
     if (dims) {
-      int d[10] = {p.first, p.B, p.T, p.VT, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size(), (int)p.gq.size(), 0};
+      int d[10] = {p.first, p.B, p.T, p.valid, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size(), (int)p.gq.size(), 0};
       memcpy(dims, d, sizeof d);
     }
     if (rows) {
       memcpy(rows, p.ids.data(), p.T * 4); memcpy(rows + p.T, p.pos.data(), p.T * 4);
-      memcpy(rows + 2 * p.T, p.seq.data(), p.T * 4); memcpy(rows + 3 * p.T, p.vcol.data(), p.T * 4);
+      memcpy(rows + 2 * p.T, p.seq.data(), p.T * 4);
     }
     if (seqs) {
       int* s = seqs;
       memcpy(s, p.soff.data(), (p.B + 1) * 4); s += p.B + 1;
       memcpy(s, p.vlen.data(), p.B * 4); s += p.B;
-      memcpy(s, p.vbase.data(), p.B * 4); s += p.B;
       memcpy(s, p.qt.data(), p.B * 4); s += p.B;
       memcpy(s, p.nm.data(), p.B * 4); s += p.B;
       memcpy(s, p.moff.data(), p.B * 4);

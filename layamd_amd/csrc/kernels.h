@@ -31,13 +31,12 @@ struct GemmArgs {
   int act = ACT_NONE;                            // EPI_STORE only
   void* C = nullptr; int ldc = 0;                // EPI_STORE: [M][ldc] T; EPI_GEGLU: [M][ldc] T, N/2 wide
   float* X = nullptr; int ldx = 0;               // EPI_RESID: X[M][ldx] += result
-  // EPI_QKV: columns [q | k | v], each H*HD wide; q and k get RoPE when rope_cos != null (the
-  // weight rows of q and k are then stored in rope-pair order, see engine.hip)
+  // EPI_QKV: columns [q | k | v], each H*HD wide; q and k get RoPE when rope_cos != null
   void* Q = nullptr; void* Kt = nullptr; int ldqk = 0;
-  void* Vt = nullptr; int ldv = 0;               // V^T [H*HD][ldv]
+  void* Vt = nullptr; int ldv = 0;               // V^T [H*HD][ldv], column = row
   int H = 0, HD = 0;
-  const int* pos = nullptr; const int* vcol = nullptr;
-  const float* rope_cos = nullptr; const float* rope_sin = nullptr;  // [max_len][HD/2]
+  const int* pos = nullptr;                      // RoPE position of each row
+  const float* rope_cos = nullptr; const float* rope_sin = nullptr;  // [positions][HD/2]
 };
 
 template <typename T>
@@ -47,11 +46,12 @@ bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
 // ---- attention over packed sequences ----
 // Query tiles from `tiles`; gathered mode when gq != null (queries are gathered rows
 // grow[gq[tile.q0 + r]], outputs go to row gq[...] of O).  window_half = 0: all keys of the
-// sequence; otherwise keys with |i - j| <= window_half.
+// sequence; otherwise keys with |i - j| <= window_half.  V^T column = packed row; sequences start
+// on 8-row boundaries and V^T has 64 columns of slack after the last row.
 template <typename T>
 void launch_attention(const T* Q, const T* K, int ldqk, const T* Vt, int ldv, T* O, int ldo, const AttnTile* tiles,
-                      int ntiles, int H, const int* soff, const int* vlen, const int* vbase, const int* gq,
-                      const int* grow, int window_half, float scale, hipStream_t st);
+                      int ntiles, int H, const int* soff, const int* vlen, const int* gq, const int* grow,
+                      int window_half, float scale, hipStream_t st);
 
 // ---- scorer tail and act head ----
 // logits[r] = dot(h[r], w) + b[0]   (fp32 accumulate)
@@ -60,8 +60,9 @@ void launch_row_dot(const T* h, int ldh, const float* w, const float* b, float* 
 
 // act head per question (ref/rl_common.py:116-123): softmax over its logits -> features
 // [top1, top1-top2, H(p)/ln(max(k,2)), max(k,2)/255] ++ cls row -> GELU(W0 . + b0) -> W2 . + b2
+// hidden: scratch [B][256] fp32
 void launch_act_head(const float* cls, int D, const float* logits, const int* moff, const int* nmark,
-                     const float* W0, const float* B0, const float* W2, const float* B2, int n_act, float* out, int B,
-                     hipStream_t st);
+                     const float* W0, const float* B0, const float* W2, const float* B2, int n_act, float* out,
+                     float* hidden, int B, hipStream_t st);
 
 }  // namespace laya

@@ -17,8 +17,8 @@
 //
 // Masks: key j of the sequence is visible to query position p when j < len and, for sliding
 // layers, |p - j| <= window_half (inclusive, HF masking_utils.py:141-151).  Keys beyond the
-// sequence are read (V^T columns up to the next 64-key boundary exist and are finite) but get
-// probability exactly 0.
+// sequence are read (V^T columns up to the next 64-key boundary exist and hold finite values:
+// padding rows, the next question, or the zero-initialised slack) but get probability exactly 0.
 #include "kernels.h"
 
 namespace laya {
@@ -32,8 +32,8 @@ template <typename T>
 __global__ __launch_bounds__(256) void k_attention(const T* __restrict__ Q, const T* __restrict__ K, int ldqk,
                                                    const T* __restrict__ Vt, int ldv, T* __restrict__ O, int ldo,
                                                    const AttnTile* __restrict__ tiles, const int* __restrict__ soff,
-                                                   const int* __restrict__ vlen, const int* __restrict__ vbase,
-                                                   const int* __restrict__ gq, const int* __restrict__ grow,
+                                                   const int* __restrict__ vlen, const int* __restrict__ gq,
+                                                   const int* __restrict__ grow,
                                                    int window_half, float scale) {
   constexpr int HD = 64;
   constexpr int CPR = HD * (int)sizeof(T) / 16;        // 16-byte chunks per 64-element row
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void k_attention(const T* __restrict__ Q, cons
   const AttnTile tile = tiles[blockIdx.x];
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const int b = tile.seq, len = vlen[b], base = soff[b], vb = vbase[b];
+  const int b = tile.seq, len = vlen[b], base = soff[b], vb = base;   // V^T column = row
 
   // this lane's query (16 per wave)
   const int r = wave * 16 + l16;
@@ -215,18 +215,17 @@ __global__ __launch_bounds__(256) void k_attention(const T* __restrict__ Q, cons
 
 template <typename T>
 void launch_attention(const T* Q, const T* K, int ldqk, const T* Vt, int ldv, T* O, int ldo, const AttnTile* tiles,
-                      int ntiles, int H, const int* soff, const int* vlen, const int* vbase, const int* gq,
-                      const int* grow, int window_half, float scale, hipStream_t st) {
+                      int ntiles, int H, const int* soff, const int* vlen, const int* gq, const int* grow,
+                      int window_half, float scale, hipStream_t st) {
   if (ntiles <= 0) return;
   hipLaunchKernelGGL((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
-                     vlen, vbase, gq, grow, window_half, scale);
+                     vlen, gq, grow, window_half, scale);
 }
 
 template void launch_attention<float>(const float*, const float*, int, const float*, int, float*, int, const AttnTile*,
-                                      int, int, const int*, const int*, const int*, const int*, const int*, int, float,
-                                      hipStream_t);
+                                      int, int, const int*, const int*, const int*, const int*, int, float, hipStream_t);
 template void launch_attention<bf16_t>(const bf16_t*, const bf16_t*, int, const bf16_t*, int, bf16_t*, int,
-                                       const AttnTile*, int, int, const int*, const int*, const int*, const int*,
-                                       const int*, int, float, hipStream_t);
+                                       const AttnTile*, int, int, const int*, const int*, const int*, const int*, int,
+                                       float, hipStream_t);
 
 }  // namespace laya

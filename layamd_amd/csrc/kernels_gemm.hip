@@ -16,11 +16,12 @@
 //   EPI_STORE  C = act(acc + bias)                        (storage type)
 //   EPI_RESID  X += acc + bias                            (fp32 residual stream)
 //   EPI_QKV    q,k (RoPE when tables are given) -> Q, K [rows][H*HD]; v -> V^T [H*HD][ldv] at
-//              column vcol[row].  With RoPE the q/k weight rows of each head are stored in the
-//              order d = [0..15, 32..47, 16..31, 48..63], so rotate_half partners (d, d+32) sit in
-//              adjacent 16-column blocks of the same lane.
-//   EPI_GEGLU  W rows stored as alternating 16-row blocks of input and gate rows; writes
+//              column = row.  A wave's column range covers whole 64-wide heads, so the
+//              rotate_half partners (d, d+32) of a row sit in the same lane.
+//   EPI_GEGLU  W rows stored as alternating 32-row blocks of input and gate rows; writes
 //              gelu_erf(input) * gate into C [rows][N/2].
+#include <cmath>
+
 #include "kernels.h"
 
 namespace laya {
@@ -163,12 +164,14 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
         }
     }
   } else if constexpr (EPI == EPI_GEGLU) {
-    static_assert(WTN % 32 == 0, "GeGLU pairs");
+    // 32-column groups [input 32 | gate 32]: block j pairs with block j + 2
+    static_assert(WTN % 64 == 0, "GeGLU pairs");
 #pragma unroll
-    for (int j = 0; j < FN; j += 2) {
+    for (int j = 0; j < FN; j++) {
+      if ((j & 3) >= 2) continue;
       const int cin = cbase + j * 16;          // first column of the input block
       if (cin + l16 >= a.N) continue;
-      const int oc = cin / 2 + l16;
+      const int oc = (cin / 64) * 32 + (cin % 64) + l16;
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
           const int row = rbase + i * 16 + e;
           if (row >= a.M) continue;
           const float x = acc[i][j][e] + (a.bias ? a.bias[cin + l16] : 0.f);
-          const float y = acc[i][j + 1][e] + (a.bias ? a.bias[cin + 16 + l16] : 0.f);
+          const float y = acc[i][j + 2][e] + (a.bias ? a.bias[cin + 32 + l16] : 0.f);
           store_elt<T>(a.C, (size_t)row * a.ldc + oc, gelu_erf(x) * y);
         }
     }
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
           for (int e = 0; e < 4; e++) {
             const int row = rbase + i * 16 + e;
             if (row >= a.M) continue;
-            Elt<T>::st(vt + a.vcol[row], acc[i][j][e] + (bb ? bb[l16] : 0.f));
+            Elt<T>::st(vt + row, acc[i][j][e] + (bb ? bb[l16] : 0.f));
           }
         continue;
       }
@@ -213,12 +216,9 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
           }
         continue;
       }
-      // rope: blocks of a head are (t=0: d 0..15), (16: d 32..47), (32: d 16..31), (48: d 48..63);
-      // the pair (a, b) = (d, d + 32) lives in blocks j and j + 1 when t is 0 or 32.
-      if (t != 0 && t != 32) continue;         // handled together with its partner block
-      if (j + 1 >= FN) continue;               // cannot happen: WTN is a multiple of 64
-      const int dlo = t == 0 ? 0 : 16;         // frequency index base and first-half dim base
-      const float* bb2 = a.bias ? a.bias + c0 + 16 : nullptr;
+      // rope: rotate_half partners (d, d + 32) are blocks j and j + 2 of the head (t = 0 or 16)
+      if (t >= 32) continue;                   // handled together with its partner block
+      const float* bb2 = a.bias ? a.bias + c0 + 32 : nullptr;
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -226,10 +226,10 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
           const int row = rbase + i * 16 + e;
           if (row >= a.M) continue;
           const int p = a.pos[row];
-          const float c = a.rope_cos[p * (a.HD / 2) + dlo + l16], s = a.rope_sin[p * (a.HD / 2) + dlo + l16];
+          const float c = a.rope_cos[p * (a.HD / 2) + t + l16], s = a.rope_sin[p * (a.HD / 2) + t + l16];
           const float x1 = acc[i][j][e] + (bb ? bb[l16] : 0.f);
-          const float x2 = acc[i][j + 1][e] + (bb2 ? bb2[l16] : 0.f);
-          T* o = dst + (size_t)row * a.ldqk + h * a.HD + dlo + l16;
+          const float x2 = acc[i][j + 2][e] + (bb2 ? bb2[l16] : 0.f);
+          T* o = dst + (size_t)row * a.ldqk + h * a.HD + t + l16;
           Elt<T>::st(o, x1 * c - x2 * s);
           Elt<T>::st(o + a.HD / 2, x2 * c + x1 * s);
         }
@@ -249,13 +249,389 @@ static void launch_cfg(int epi, const GemmArgs& a, hipStream_t st) {
   }
 }
 
+
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// Adjacent lanes hold adjacent columns; each lane holds rows r and r+1 of its column (ve, ve1).
+// One DPP swap (quad_perm 1,0,3,2 = lane ^ 1) gives the even lane row r of columns (c, c+1) and
+// the odd lane row r+1 of columns (c-1, c), packed as bf16 pairs.
+__device__ __forceinline__ uint32_t pair_rows_to_cols(float ve, float ve1, bool odd) {
+  const float send = odd ? ve : ve1;
+  const float recv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+  return odd ? pk_bf16(recv, ve1) : pk_bf16(ve, recv);
+}
+
+// ======================================================================================
+// Large-tile bf16 GEMM (v_mfma_f32_32x32x16_bf16).  A workgroup of 4 wave64s computes a
+// BM x BN tile (256x256 by default, one workgroup per CU, 128 KiB of LDS for two K stages);
+// each wave owns a (BM/WM) x (BN/WN) sub-tile held in 32x32 accumulator blocks, so one
+// 16-byte LDS fragment feeds 4 MFMAs and LDS traffic stays well under the MFMA rate.
+// Global loads go through buffer resources: rows beyond M (or N) fall outside the resource and
+// read as zero, so partial tiles need no clamping.  Tiles are ordered in groups of 8 tile rows
+// inside each XCD's contiguous range so the tiles running at once on an XCD share A rows and
+// W columns in its L2.
+//
+// 32x32 accumulator layout: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, col l%32.
+// A/B operand: lane l holds 8 consecutive K values of row (col) l%32, K offset 8*(l/32).
+// ======================================================================================
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void tile_coords(int bid, int tilesM, int tilesN, int& tm, int& tn) {
+  const int p = xcd_remap(bid, tilesM * tilesN);
+  constexpr int G = 8;
+  const int per = G * tilesN, first = (p / per) * G, gs = min(tilesM - first, G), r = p % per;
+  tm = first + r % gs;
+  tn = r / gs;
+}
+
+// LDS fill by DMA: buffer_load_dwordx4 ... lds writes lane l's 16 bytes to LDS at (M0 base) +
+// 16*l, so each wave instruction fills 64 consecutive chunks = 8 tile rows.  The swizzle is
+// applied on the global side: the lane landing at row r, chunk position c loads global chunk
+// c ^ (r & 7).  Rows past M (or N) lie outside the buffer resource and arrive as zeros.
+template <int ROWS>
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rsrc, u32x4_t* lds, int row0, int ld_bytes, int kbyte,
+                                         int wave, int lane) {
+  constexpr int PER_WAVE = ROWS / 32;                  // instructions per wave (8 rows each)
+  const int rl = lane >> 3, cpos = lane & 7;
+#pragma unroll
+  for (int j = 0; j < PER_WAVE; j++) {
+    const int r = (wave * PER_WAVE + j) * 8 + rl;
+    const int voff = (row0 + r) * ld_bytes + ((cpos ^ (r & 7)) << 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds + (wave * PER_WAVE + j) * 64),
+                                             16, voff, kbyte, 0, 0);
+  }
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void load_frags(const u32x4_t* As, const u32x4_t* Bs, int arow, int brow, int s, int lane,
+                                           u32x4_t (&af)[FM], u32x4_t (&bf)[FN]) {
+  const int ch = (2 * s + (lane >> 5)) ^ (lane & 7);
+#pragma unroll
+  for (int i = 0; i < FM; i++) af[i] = As[(arow + i * 32) * 8 + ch];
+#pragma unroll
+  for (int j = 0; j < FN; j++) bf[j] = Bs[(brow + j * 32) * 8 + ch];
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void mma_step(f32x16_t (&acc)[FM][FN], const u32x4_t (&af)[FM], const u32x4_t (&bf)[FN]) {
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
+                                                          __builtin_bit_cast(bf16x8_t, bf[j]), acc[i][j], 0, 0, 0);
+}
+
+// one 64-deep K slice from one LDS stage: 4 steps of 16, fragments double-buffered in registers
+template <int FM, int FN>
+__device__ __forceinline__ void mma_slice(f32x16_t (&acc)[FM][FN], const u32x4_t* As, const u32x4_t* Bs, int arow,
+                                          int brow, int lane) {
+  u32x4_t a0[FM], b0[FN], a1[FM], b1[FN];
+  load_frags<FM, FN>(As, Bs, arow, brow, 0, lane, a0, b0);
+  load_frags<FM, FN>(As, Bs, arow, brow, 1, lane, a1, b1);
+  mma_step<FM, FN>(acc, a0, b0);
+  load_frags<FM, FN>(As, Bs, arow, brow, 2, lane, a0, b0);
+  mma_step<FM, FN>(acc, a1, b1);
+  load_frags<FM, FN>(As, Bs, arow, brow, 3, lane, a1, b1);
+  mma_step<FM, FN>(acc, a0, b0);
+  mma_step<FM, FN>(acc, a1, b1);
+}
+
+template <int BM, int BN, int WM, int WN, int EPI, int ACT>
+__global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
+  using T = bf16_t;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
+  __shared__ u32x4_t As0[BM * 8], As1[BM * 8];      // two K stages, separate objects so the
+  __shared__ u32x4_t Bs0[BN * 8], Bs1[BN * 8];      // compiler sees DMA and reads never alias
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
+  const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
+  int tm, tn;
+  tile_coords(blockIdx.x, tilesM, tilesN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.A), (short)0, (int)((size_t)a.M * a.lda * sizeof(T)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.W), (short)0, (int)((size_t)a.N * a.ldw * sizeof(T)), 0x00020000);
+  const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
+
+  f32x16_t acc[FM][FN];
+  if constexpr (EPI == EPI_RESID) {
+    // the residual update X += A W^T + b starts the accumulators at X (rows/cols outside X read 0),
+    // so the epilogue issues no global load after its first store
+    const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
+        a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
+    const int r0 = m0 + wm * WTM + 4 * hi, c0 = n0 + wn * WTN + l32;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int row = r0 + i * 32 + 8 * (e >> 2) + (e & 3), col = c0 + j * 32;
+          const int off = col < a.N ? (row * a.ldx + col) * 4 : 0x7FFFFFF0;
+          acc[i][j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rX, off, 0, 0));
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+  }
+
+  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
+  const int nk = a.K / 64;
+  dma_tile<BM>(rA, As0, m0, lda_b, 0, wave, lane);
+  dma_tile<BN>(rB, Bs0, n0, ldw_b, 0, wave, lane);
+  __syncthreads();
+  // pairs of K slices with both stages unconditional (keeps the accumulators in place), then an
+  // odd tail from stage 0
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    dma_tile<BM>(rA, As1, m0, lda_b, (kt + 1) * 128, wave, lane);
+    dma_tile<BN>(rB, Bs1, n0, ldw_b, (kt + 1) * 128, wave, lane);
+    mma_slice<FM, FN>(acc, As0, Bs0, arow, brow, lane);
+    __syncthreads();
+    if (kt + 2 < nk) {
+      dma_tile<BM>(rA, As0, m0, lda_b, (kt + 2) * 128, wave, lane);
+      dma_tile<BN>(rB, Bs0, n0, ldw_b, (kt + 2) * 128, wave, lane);
+    }
+    mma_slice<FM, FN>(acc, As1, Bs1, arow, brow, lane);
+    __syncthreads();
+  }
+  if (kt < nk) mma_slice<FM, FN>(acc, As0, Bs0, arow, brow, lane);
+
+  // ---------------- epilogue ----------------
+  // On gfx9 vmcnt counts stores as well as loads, so a global load issued after a store waits for
+  // that store.  The epilogue therefore loads everything it needs (bias, positions, RoPE tables)
+  // before its first store: residual updates started their accumulators at X above and only add
+  // a preloaded bias; the other epilogues finish every value of the wave's tile into LDS first
+  // (bf16, the K stages are idle) and then stream it out as 16-byte row segments.
+  __syncthreads();
+  const int rbase = m0 + wm * WTM, cbase = n0 + wn * WTN;
+  auto pack8 = [](float4 x, float4 y) {
+    u32x4_t u;
+    u[0] = (uint32_t)f2bf(x.x) | ((uint32_t)f2bf(x.y) << 16);
+    u[1] = (uint32_t)f2bf(x.z) | ((uint32_t)f2bf(x.w) << 16);
+    u[2] = (uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16);
+    u[3] = (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16);
+    return u;
+  };
+  if constexpr (EPI == EPI_RESID) {
+    // per 32 x 64 block through an fp32 scratch of 8 KiB per wave; no loads in the loop
+    float* scr = reinterpret_cast<float*>(wave < 2 ? As0 : As1) + (wave & 1) * 2048;
+    auto sidx = [](int r, int c) { return r * 64 + ((((c >> 2) ^ (r & 15))) << 2) + (c & 3); };
+    float bias[FN];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = cbase + j * 32 + l32;
+      bias[j] = (a.bias && col < a.N) ? a.bias[col] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int jp = 0; jp < FN; jp += 2) {
+        const int row0 = rbase + i * 32, c0 = cbase + jp * 32;
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) scr[sidx(8 * (e >> 2) + 4 * hi + (e & 3), 32 * b + l32)] = acc[i][jp + b][e] + bias[jp + b];
+        __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+          const int item = lane + 64 * it, r = item >> 4, q = item & 15;
+          const int row = row0 + r, col = c0 + 4 * q;
+          if (row < a.M && col < a.N)
+            *reinterpret_cast<float4*>(a.X + (size_t)row * a.ldx + col) =
+                *reinterpret_cast<const float4*>(scr + r * 64 + ((q ^ (r & 15)) << 2));
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  } else {
+    // phase 1: the wave's finished tile -> LDS as bf16, [WTM][OW] with 16-byte chunks swizzled by row
+    constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;     // output columns of the wave tile
+    constexpr int CPRW = OW / 8;                             // 16-byte chunks per row
+    bf16_t* wt = reinterpret_cast<bf16_t*>(wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? Bs0 : Bs1);
+    auto oidx = [](int r, int c) { return r * OW + ((((c >> 3) ^ (r & 7)) & (CPRW - 1)) << 3) + (c & 7); };
+    const bool odd = lane & 1;
+    // element e of a 32x32 block is row 8*(e/4) + 4*hi + e%4: elements (e, e+1), e even, are rows
+    // (r, r+1) of column l32; after the pair swap this lane writes 4 bytes at (r + odd, l32 & ~1)
+    auto put = [&](int i, int e, int cblk, float ve, float ve1) {
+      const int r = i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3) + (odd ? 1 : 0);
+      *reinterpret_cast<uint32_t*>(wt + oidx(r, cblk + (l32 & ~1))) = pair_rows_to_cols(ve, ve1, odd);
+    };
+    const int D = a.H * a.HD;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int jp = 0; jp < FN; jp += 2) {
+        const int c0 = cbase + jp * 32;
+        if constexpr (EPI == EPI_GEGLU) {
+          const bool ok = c0 < a.N;
+          const float bx = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, by = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; e += 2)
+            put(i, e, jp * 16, gelu_erf(acc[i][jp][e] + bx) * (acc[i][jp + 1][e] + by),
+                gelu_erf(acc[i][jp][e + 1] + bx) * (acc[i][jp + 1][e + 1] + by));
+        } else if constexpr (EPI == EPI_QKV) {
+          const bool ok = c0 < a.N;
+          const float b0 = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, b1 = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
+          if (a.rope_cos && c0 < 2 * D) {
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+              float o1[2], o2[2];
+#pragma unroll
+              for (int u = 0; u < 2; u++) {
+                const int r = i * 32 + 8 * ((e + u) >> 2) + 4 * hi + ((e + u) & 3);
+                const int p = a.pos[min(rbase + r, a.M - 1)];
+                const float c = a.rope_cos[p * 32 + l32], sn = a.rope_sin[p * 32 + l32];
+                const float x1 = acc[i][jp][e + u] + b0, x2 = acc[i][jp + 1][e + u] + b1;
+                o1[u] = x1 * c - x2 * sn;
+                o2[u] = x2 * c + x1 * sn;
+              }
+              put(i, e, jp * 32, o1[0], o1[1]);
+              put(i, e, jp * 32 + 32, o2[0], o2[1]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+              put(i, e, jp * 32, acc[i][jp][e] + b0, acc[i][jp][e + 1] + b0);
+              put(i, e, jp * 32 + 32, acc[i][jp + 1][e] + b1, acc[i][jp + 1][e + 1] + b1);
+            }
+          }
+        } else {  // EPI_STORE
+#pragma unroll
+          for (int b = 0; b < 2; b++) {
+            const int col = c0 + 32 * b + l32;
+            const float bb = (a.bias && col < a.N) ? a.bias[col] : 0.f;
+            auto f = [&](float v) {
+              v += bb;
+              if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
+              if constexpr (ACT == ACT_GELU) v = gelu_erf(v);
+              return v;
+            };
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) put(i, e, (jp + b) * 32, f(acc[i][jp + b][e]), f(acc[i][jp + b][e + 1]));
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    // phase 2: stores only
+    if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+      for (int hb = 0; hb < WTN / 64; hb++) {                // one 64-column head block at a time
+        const int c0 = cbase + hb * 64;
+        if (c0 >= a.N) break;
+        const int sec = c0 / D, h = (c0 % D) / a.HD;
+        if (sec == 2) {                                      // V^T: 8 consecutive rows of one column
+          T* vt = reinterpret_cast<T*>(a.Vt) + (size_t)h * a.HD * a.ldv;
+#pragma unroll
+          for (int it = 0; it < WTM / 8; it++) {
+            const int item = lane + 64 * it, c = item >> (WTM == 128 ? 4 : 3), rg = item & (WTM / 8 - 1);
+            const int row = rbase + 8 * rg;
+            if (row >= a.M) continue;
+            uint32_t u[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+              u[t] = (uint32_t)wt[oidx(8 * rg + 2 * t, hb * 64 + c)] | ((uint32_t)wt[oidx(8 * rg + 2 * t + 1, hb * 64 + c)] << 16);
+            T* dst = vt + (size_t)c * a.ldv + row;
+            if (row + 7 < a.M) {
+              *reinterpret_cast<u32x4_t*>(dst) = (u32x4_t){u[0], u[1], u[2], u[3]};
+            } else {
+              for (int t = 0; t < 8 && row + t < a.M; t++) dst[t] = (bf16_t)(u[t >> 1] >> (16 * (t & 1)));
+            }
+          }
+        } else {
+          T* base = reinterpret_cast<T*>(sec == 0 ? a.Q : a.Kt) + h * a.HD;
+#pragma unroll
+          for (int it = 0; it < WTM / 8; it++) {
+            const int item = lane + 64 * it, r = item >> 3, q = item & 7;
+            const int row = rbase + r;
+            if (row < a.M)
+              *reinterpret_cast<u32x4_t*>(base + (size_t)row * a.ldqk + 8 * q) =
+                  *reinterpret_cast<const u32x4_t*>(wt + oidx(r, hb * 64 + 8 * q));
+          }
+        }
+      }
+    } else {
+      const int ocol0 = EPI == EPI_GEGLU ? cbase / 2 : cbase;
+      const int ncols = EPI == EPI_GEGLU ? a.N / 2 : a.N;
+#pragma unroll
+      for (int it = 0; it < WTM * CPRW / 64; it++) {
+        const int item = lane + 64 * it, r = item / CPRW, q = item % CPRW;
+        const int row = rbase + r, col = ocol0 + 8 * q;
+        if (row < a.M && col < ncols)
+          *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.C) + (size_t)row * a.ldc + col) =
+              *reinterpret_cast<const u32x4_t*>(wt + oidx(r, 8 * q));
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN>
+static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (epi == EPI_STORE) {
+    if (a.act == ACT_RELU) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_RELU>), dim3(tiles), dim3(256), 0, st, a);
+    else if (a.act == ACT_GELU) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_GELU>), dim3(tiles), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a);
+    return;
+  }
+  switch (epi) {
+    case EPI_RESID: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_RESID, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_QKV: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_QKV, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_GEGLU: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_GEGLU, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    default: fprintf(stderr, "[laya] gemm: bad epilogue %d\n", epi); exit(1);
+  }
+}
+
+// Tile configurations for the bf16 path and the planner that picks one per GEMM: estimated time
+// = rounds of concurrently resident tiles x per-tile cost, with the per-CU throughput of each
+// shape relative to 256x256.  Measured on MI355X at the ModernBERT-large shapes: two resident
+// 128x128 workgroups per CU (64 KiB of LDS each) beat one 256x256 workgroup by ~1.4x, because
+// one workgroup's epilogue (LDS staging, GELU/RoPE math, output stores) overlaps the other's
+// MFMA main loop, while a lone 256x256 workgroup leaves the MFMA pipe idle during its epilogue.
+struct XlCfg { int bm, bn, per_cu; float rel; };
+static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.90f}, {128, 256, 1, 0.90f}, {128, 128, 2, 1.40f}};
+
+int gemm_pick(int M, int N, int /*epi*/) {
+  int best = -1;
+  double bt = 1e300;
+  for (int i = 0; i < (int)(sizeof(kXl) / sizeof(kXl[0])); i++) {
+    const XlCfg& c = kXl[i];
+    const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const double slots = 256.0 * c.per_cu;
+    const double t = std::ceil(tiles / slots) * (double)c.bm * c.bn * c.per_cu / c.rel;
+    if (t < bt * 0.999) { bt = t; best = i; }
+  }
+  return best;
+}
+
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) {
   const int bk = 128 / elt_bytes, align = 16 / elt_bytes;
   if (a.M <= 0 || a.N <= 0) { *why = "empty"; return false; }
   if (a.K <= 0 || a.K % bk) { *why = "K must be a positive multiple of the 128-byte K slice"; return false; }
   if (a.lda % align || a.ldw % align || a.lda < a.K || a.ldw < a.K) { *why = "row strides must be 16-byte multiples >= K"; return false; }
   if ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W)) & 15) { *why = "operands must be 16-byte aligned"; return false; }
-  if (epi == EPI_GEGLU && a.N % 32) { *why = "GeGLU needs N % 32 == 0"; return false; }
+  if (epi == EPI_GEGLU && a.N % 64) { *why = "GeGLU needs N % 64 == 0"; return false; }
   if (epi == EPI_QKV) {
     if (a.N != 3 * a.H * a.HD || a.HD % 16) { *why = "QKV needs N == 3*H*HD, HD % 16 == 0"; return false; }
     if (a.rope_cos && a.HD != 64) { *why = "fused RoPE needs HD == 64"; return false; }
@@ -269,6 +645,23 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
   if (!gemm_shape_ok(epi, a, (int)sizeof(T), &why)) {
     fprintf(stderr, "[laya] gemm %dx%dx%d epi %d rejected: %s\n", a.M, a.N, a.K, epi, why);
     exit(1);
+  }
+  if constexpr (sizeof(T) == 2) {
+    const size_t abytes = (size_t)a.M * a.lda * sizeof(T), wbytes = (size_t)a.N * a.ldw * sizeof(T);
+    // 16-byte epilogue stores need N, the row strides and the output bases in multiples of 8 elements
+    const bool aligned = a.N % 8 == 0 && ((epi == EPI_STORE || epi == EPI_GEGLU) ? a.ldc % 8 == 0 : true) &&
+                         (epi == EPI_RESID ? a.ldx % 4 == 0 : true) && (epi == EPI_QKV ? a.ldqk % 8 == 0 && a.ldv % 8 == 0 : true);
+    const bool xl_ok = aligned && abytes < (1u << 31) - 65536 && wbytes < (1u << 31) - 65536;
+    if (xl_ok) {
+      // LAYA_GEMM_CFG=0..3 pins one tile configuration (256x256, 256x128, 128x256, 128x128)
+      static const int forced = getenv("LAYA_GEMM_CFG") ? atoi(getenv("LAYA_GEMM_CFG")) : -1;
+      switch (forced >= 0 && forced < 4 ? forced : gemm_pick(a.M, a.N, epi)) {
+        case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;
+        case 1: launch_xl<256, 128, 2, 2>(epi, a, st); return;
+        case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
+        default: launch_xl<128, 128, 2, 2>(epi, a, st); return;
+      }
+    }
   }
   launch_cfg<T, 128, 128, 2, 2>(epi, a, st);
 }

@@ -131,20 +131,18 @@ void launch_row_dot(const T* h, int ldh, const float* w, const float* b, float* 
 template void launch_row_dot<float>(const float*, int, const float*, const float*, float*, int, int, hipStream_t);
 template void launch_row_dot<bf16_t>(const bf16_t*, int, const float*, const float*, float*, int, int, hipStream_t);
 
-// ---- act head: one 256-thread workgroup per question ----
-// Follows ref/rl_common.py:116-123: p = softmax(logits over the question's markers); k =
-// max(nmark, 2); features [top1, top1 - top2, -sum p log(max(p, 1e-9)) / ln k, k / 255];
-// hidden = GELU(W0 [cls, features] + b0) with W0 [256][D + 4]; out = W2 hidden + b2.
-__global__ __launch_bounds__(256) void k_act_head(const float* __restrict__ cls, int D, const float* __restrict__ logits,
-                                                  const int* __restrict__ moff, const int* __restrict__ nmark,
-                                                  const float* __restrict__ W0, const float* __restrict__ B0,
-                                                  const float* __restrict__ W2, const float* __restrict__ B2, int n_act,
-                                                  float* __restrict__ out) {
-  extern __shared__ float sm[];
-  float* in = sm;               // D + 4
-  float* hid = sm + D + 4;      // 256
+// ---- act head (ref/rl_common.py:116-123) ----
+// p = softmax(logits over the question's markers); k = max(nmark, 2); features [top1,
+// top1 - top2, -sum p log(max(p, 1e-9)) / ln k, k / 255]; hidden = GELU(W0 [cls, features] + b0)
+// with W0 [256][D + 4]; out = W2 hidden + b2.
+// k_act_hidden: grid (B, 16); each workgroup recomputes the question's 4 features (<= 255 logits)
+// and produces 16 hidden units, one wave per 4 units with lanes striding over D + 4.
+__global__ __launch_bounds__(256) void k_act_hidden(const float* __restrict__ cls, int D, const float* __restrict__ logits,
+                                                    const int* __restrict__ moff, const int* __restrict__ nmark,
+                                                    const float* __restrict__ W0, const float* __restrict__ B0,
+                                                    float* __restrict__ hidden) {
+  __shared__ float feat[4];
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  for (int d = t; d < D; d += 256) in[d] = cls[(size_t)b * D + d];
   if (t == 0) {
     const float* z = logits + moff[b];
     const int K = nmark[b];
@@ -159,31 +157,40 @@ __global__ __launch_bounds__(256) void k_act_head(const float* __restrict__ cls,
       if (p > t1) { t2 = t1; t1 = p; } else if (p > t2) t2 = p;
     }
     const float k = (float)(K < 2 ? 2 : K);
-    in[D] = t1; in[D + 1] = t1 - t2; in[D + 2] = ent / logf(k); in[D + 3] = k / 255.f;
+    feat[0] = t1; feat[1] = t1 - t2; feat[2] = ent / logf(k); feat[3] = k / 255.f;
   }
   __syncthreads();
-  for (int j = wv; j < 256; j += 4) {
+  const float* c = cls + (size_t)b * D;
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int j = blockIdx.y * 16 + wv * 4 + u;
     const float* wr = W0 + (size_t)j * (D + 4);
     float a = 0.f;
-    for (int i = lane; i < D + 4; i += 64) a += wr[i] * in[i];
+    for (int i = lane; i < D; i += 64) a += wr[i] * c[i];
+    if (lane < 4) a += wr[D + lane] * feat[lane];
     a = wave_sum(a);
-    if (lane == 0) hid[j] = gelu_erf(a + B0[j]);
+    if (lane == 0) hidden[(size_t)b * 256 + j] = gelu_erf(a + B0[j]);
   }
-  __syncthreads();
-  for (int j = wv; j < n_act; j += 4) {
-    const float* wr = W2 + (size_t)j * 256;
+}
+
+// k_act_out: one wave per question, out[b][t] = W2[t] . hidden[b] + b2[t]
+__global__ __launch_bounds__(64) void k_act_out(const float* __restrict__ hidden, const float* __restrict__ W2,
+                                                const float* __restrict__ B2, int n_act, float* __restrict__ out) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  for (int j = 0; j < n_act; j++) {
     float a = 0.f;
-    for (int i = lane; i < 256; i += 64) a += wr[i] * hid[i];
+    for (int i = lane; i < 256; i += 64) a += W2[(size_t)j * 256 + i] * hidden[(size_t)b * 256 + i];
     a = wave_sum(a);
     if (lane == 0) out[(size_t)b * n_act + j] = a + B2[j];
   }
 }
 
 void launch_act_head(const float* cls, int D, const float* logits, const int* moff, const int* nmark, const float* W0,
-                     const float* B0, const float* W2, const float* B2, int n_act, float* out, int B, hipStream_t st) {
+                     const float* B0, const float* W2, const float* B2, int n_act, float* out, float* hidden, int B,
+                     hipStream_t st) {
   if (B <= 0) return;
-  hipLaunchKernelGGL(k_act_head, dim3(B), dim3(256), (D + 4 + 256) * sizeof(float), st, cls, D, logits, moff, nmark, W0,
-                     B0, W2, B2, n_act, out);
+  hipLaunchKernelGGL(k_act_hidden, dim3(B, 16), dim3(256), 0, st, cls, D, logits, moff, nmark, W0, B0, hidden);
+  hipLaunchKernelGGL(k_act_out, dim3(B), dim3(64), 0, st, hidden, W2, B2, n_act, out);
 }
 
 }  // namespace laya

@@ -10,6 +10,7 @@ static inline int align_up(int x, int a) { return (x + a - 1) / a * a; }
 
 int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
                 const PackLimits& lim, std::vector<PassPlan>* passes) {
+  const int pad_id = lim.pad_id;
   passes->clear();
   if (B < 0) return -1;
   std::vector<int64_t> ioff(B + 1, 0), moff(B + 1, 0);
@@ -28,30 +29,30 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
         if (t < 0 || t >= lim.vocab) return -1;
       }
   }
-  const int pass_rows = std::max(lim.pass_tokens, lim.max_len);
+  const int pass_rows = std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign));
   int b0 = 0;
   while (b0 < B) {
     int n = 0, T = 0, R = 0;
-    while (b0 + n < B && n < lim.max_seqs && T + lens[b0 + n] <= pass_rows &&
+    while (b0 + n < B && n < lim.max_seqs && T + align_up(lens[b0 + n], kRowAlign) <= pass_rows &&
            R + nmark[b0 + n] + 1 <= std::max(lim.max_grows, kMaxMarkers + 1)) {
-      T += lens[b0 + n]; R += nmark[b0 + n] + 1; n++;
+      T += align_up(lens[b0 + n], kRowAlign); R += nmark[b0 + n] + 1; n++;
     }
     PassPlan p;
     p.first = b0; p.B = n; p.T = T;
-    p.ids.resize(T); p.pos.resize(T); p.seq.resize(T); p.vcol.resize(T);
-    p.soff.resize(n + 1); p.vlen.resize(n); p.vbase.resize(n); p.qt.resize(n); p.nm.resize(n); p.moff.resize(n);
-    int r = 0, vc = 0, kt = 0;
+    p.ids.resize(T); p.pos.resize(T); p.seq.resize(T);
+    p.soff.resize(n + 1); p.vlen.resize(n); p.qt.resize(n); p.nm.resize(n); p.moff.resize(n);
+    int r = 0, kt = 0;
     for (int i = 0; i < n; i++) {
-      const int b = b0 + i, len = lens[b];
-      p.soff[i] = r; p.vlen[i] = len; p.vbase[i] = vc; p.qt[i] = qtypes[b]; p.nm[i] = nmark[b]; p.moff[i] = kt;
-      for (int j = 0; j < len; j++) {
-        p.ids[r + j] = ids[ioff[b] + j]; p.pos[r + j] = j; p.seq[r + j] = i; p.vcol[r + j] = vc + j;
+      const int b = b0 + i, len = lens[b], rows = align_up(len, kRowAlign);
+      p.soff[i] = r; p.vlen[i] = len; p.qt[i] = qtypes[b]; p.nm[i] = nmark[b]; p.moff[i] = kt;
+      for (int j = 0; j < rows; j++) {
+        p.ids[r + j] = j < len ? ids[ioff[b] + j] : pad_id; p.pos[r + j] = j; p.seq[r + j] = i;
       }
       for (int q0 = 0; q0 < len; q0 += kQTile) p.tiles.push_back({i, q0, std::min(kQTile, len - q0), 0});
-      r += len; vc += align_up(len, kVAlign); kt += nmark[b];
+      r += rows; kt += nmark[b]; p.valid += len;
     }
     p.soff[n] = r;
-    p.VT = vc; p.KT = kt; p.R = kt + n;
+    p.KT = kt; p.R = kt + n;
     p.grow.resize(p.R);
     for (int i = 0; i < n; i++) {
       const int b = b0 + i;
@@ -75,9 +76,8 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
 
 PassCaps pass_caps(const PackLimits& lim) {
   PassCaps c;
-  const int64_t rows = std::max(lim.pass_tokens, lim.max_len);
+  const int64_t rows = std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign));
   c.rows = rows;
-  c.vt_cols = rows + (int64_t)lim.max_seqs * kVAlign + 64;  // alignment gaps + one key block of slack
   c.tiles = rows / kQTile + lim.max_seqs;
   c.grows = std::max(lim.max_grows, kMaxMarkers + 1);
   c.gtiles = c.grows / kQTile + lim.max_seqs;

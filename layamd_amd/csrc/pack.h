@@ -5,9 +5,11 @@
 // [0, len)), questions taken greedily in order into passes, each question its own sequence,
 // outputs unpacked per question.  The layout inside a pass is this engine's own:
 //
-//   * rows are packed densely: question i owns rows [soff[i], soff[i] + len[i]); no padding rows;
-//   * V is stored transposed per head, [H][head_dim][VT]; question i's keys start at column
-//     vbase[i] (a multiple of 16), so the attention kernel's 16-byte loads stay aligned;
+//   * rows are packed back to back with each question starting on a multiple of kRowAlign rows:
+//     question i owns rows [soff[i], soff[i] + len[i]) and up to kRowAlign - 1 padding rows after
+//     them (pad token, positions continuing past len); padding rows are computed and never read,
+//     and every aligned group of kRowAlign rows belongs to one question, so the GEMM epilogue can
+//     write V^T [H][head_dim][rows] (column = row) with 16-byte stores;
 //   * attention work is a list of query tiles (seq, first query, query count) of <= 64 queries;
 //   * the last head layer works on R = KT + B gathered rows: the KT = sum(nmark) marker rows
 //     in question order, then one CLS row per question; gathered query tiles index a list of
@@ -20,7 +22,7 @@ namespace laya {
 
 constexpr int kMaxMarkers = 255;     // options per question (the act head encodes k/255)
 constexpr int kQTile = 64;           // queries per attention tile
-constexpr int kVAlign = 16;          // column alignment of each question's keys in V^T
+constexpr int kRowAlign = 8;         // rows per aligned group (first row of every question)
 
 struct PackLimits {
   int max_len = 512;
@@ -28,15 +30,17 @@ struct PackLimits {
   int max_seqs = 512;                // questions per pass
   int max_grows = 32768;             // gathered rows (sum of nmark + 1) per pass
   int vocab = 0;                     // > 0: ids must lie in [0, vocab)
+  int pad_id = 0;                    // token id of padding rows
 };
 
 struct AttnTile { int32_t seq, q0, nq, pad; };
 
 struct PassPlan {
   int first = 0, B = 0;              // questions [first, first + B) of the call
-  int T = 0, VT = 0, KT = 0, R = 0;  // rows, V^T columns, marker rows, gathered rows
-  std::vector<int32_t> ids, pos, seq, vcol;                 // [T]
-  std::vector<int32_t> soff, vlen, vbase, qt, nm, moff;     // [B] (soff has B + 1)
+  int T = 0, KT = 0, R = 0;          // rows (padding included), marker rows, gathered rows
+  int valid = 0;                     // sum of lens
+  std::vector<int32_t> ids, pos, seq;                       // [T]
+  std::vector<int32_t> soff, vlen, qt, nm, moff;            // [B] (soff has B + 1)
   std::vector<AttnTile> tiles;                              // encoder / head-0 query tiles
   std::vector<AttnTile> gtiles;                             // gathered query tiles
   std::vector<int32_t> gq;                                  // gathered ids referenced by gtiles
@@ -44,11 +48,12 @@ struct PassPlan {
 };
 
 // Validates the call; returns 0 and fills `passes`, or -1 on an invalid input.
+// Passes hold at most pass_tokens rows, padding rows included.
 int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
                 const PackLimits& lim, std::vector<PassPlan>* passes);
 
 // Largest sizes a pass can reach under `lim` (for buffer allocation).
-struct PassCaps { int64_t rows, vt_cols, tiles, gtiles, grows; };
+struct PassCaps { int64_t rows, tiles, gtiles, grows; };
 PassCaps pass_caps(const PackLimits& lim);
 
 }  // namespace laya

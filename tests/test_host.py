@@ -21,7 +21,7 @@ def host():
         build.build()
     L = ctypes.CDLL(le.HOST_LIB)
     IP = ctypes.POINTER(ctypes.c_int)
-    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 6 + [IP] * 7
+    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 7 + [IP] * 7
     L.laya_host_plan.restype = ctypes.c_int
     L.laya_host_config.argtypes = [ctypes.c_char_p, IP, ctypes.POINTER(ctypes.c_float), ctypes.c_char_p, ctypes.c_int]
     L.laya_host_config.restype = ctypes.c_int
@@ -37,31 +37,32 @@ def P(a):
     return a, a.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
 
 
-def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=512, max_grows=32768, vocab=0):
+def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=512, max_grows=32768, vocab=0,
+         pad_id=0):
     keep = [P(x if len(x) else [0]) for x in (lens, ids, nm, mk, qt)]
-    n = host.laya_host_plan(len(lens), *[k[1] for k in keep], max_len, pass_tokens, max_seqs, max_grows, vocab, -1,
-                            *([None] * 7))
+    args = (max_len, pass_tokens, max_seqs, max_grows, vocab, pad_id)
+    n = host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, -1, *([None] * 7))
     if n < 0:
         return None
     out = []
-    T = int(np.sum(lens)) + 1
+    T = int(np.sum((np.asarray(lens) + 7) // 8 * 8)) + 1
     R = int(np.sum(nm)) + len(lens) + 1
     for w in range(n):
         dims = np.zeros(10, np.int32)
-        rows = np.zeros(4 * T, np.int32)
-        seqs = np.zeros(6 * len(lens) + 1, np.int32)
+        rows = np.zeros(3 * T, np.int32)
+        seqs = np.zeros(5 * len(lens) + 1, np.int32)
         tiles = np.zeros(4 * (T // 64 + len(lens) + 1), np.int32)
         gtiles = np.zeros(4 * (R // 64 + len(lens) + 1), np.int32)
         gq = np.zeros(R, np.int32)
         grow = np.zeros(R, np.int32)
         bufs = [P(x)[1] for x in (dims, rows, seqs, tiles, gtiles, gq, grow)]
-        host.laya_host_plan(len(lens), *[k[1] for k in keep], max_len, pass_tokens, max_seqs, max_grows, vocab, w, *bufs)
-        first, B, Tn, VT, KT, Rn, nt, ngt, ngq, _ = dims
-        s = seqs[:6 * B + 1]
-        out.append(dict(first=first, B=B, T=Tn, VT=VT, KT=KT, R=Rn,
-                        ids=rows[:Tn], pos=rows[Tn:2 * Tn], seq=rows[2 * Tn:3 * Tn], vcol=rows[3 * Tn:4 * Tn],
-                        soff=s[:B + 1], vlen=s[B + 1:2 * B + 1], vbase=s[2 * B + 1:3 * B + 1],
-                        qt=s[3 * B + 1:4 * B + 1], nm=s[4 * B + 1:5 * B + 1], moff=s[5 * B + 1:6 * B + 1],
+        host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, w, *bufs)
+        first, B, Tn, valid, KT, Rn, nt, ngt, ngq, _ = dims
+        s = seqs[:5 * B + 1]
+        out.append(dict(first=first, B=B, T=Tn, valid=valid, KT=KT, R=Rn,
+                        ids=rows[:Tn], pos=rows[Tn:2 * Tn], seq=rows[2 * Tn:3 * Tn],
+                        soff=s[:B + 1], vlen=s[B + 1:2 * B + 1], qt=s[2 * B + 1:3 * B + 1],
+                        nm=s[3 * B + 1:4 * B + 1], moff=s[4 * B + 1:5 * B + 1],
                         tiles=tiles[:4 * nt].reshape(-1, 4), gtiles=gtiles[:4 * ngt].reshape(-1, 4),
                         gq=gq[:ngq], grow=grow[:Rn]))
     return out
@@ -85,24 +86,25 @@ def test_validation_minus_one(host):
 def test_layout_of_a_pass(host):
     cfg = ck.PRESETS["tiny"]
     b = wl.make_batch(cfg, [1, 64, 65, 200, 17], [1, 3, 255, 12, 2], seed=1)
-    (p,) = plan(host, *b.flat(), max_len=320)
-    assert p["B"] == 5 and p["T"] == int(b.lens.sum())
-    soff = np.concatenate([[0], np.cumsum(b.lens)])
+    (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id)
+    rows8 = (b.lens + 7) // 8 * 8                                          # questions start on 8-row groups
+    assert p["B"] == 5 and p["T"] == int(rows8.sum()) and p["valid"] == int(b.lens.sum())
+    soff = np.concatenate([[0], np.cumsum(rows8)])
     assert np.array_equal(p["soff"], soff)
-    assert np.array_equal(p["ids"], np.concatenate(b.ids))
     for i in range(b.B):
         r = slice(soff[i], soff[i + 1])
-        assert np.array_equal(p["pos"][r], np.arange(b.lens[i]))
+        assert np.array_equal(p["ids"][r][:b.lens[i]], b.ids[i])
+        assert np.all(p["ids"][r][b.lens[i]:] == cfg.pad_id)               # padding rows: pad token
+        assert np.array_equal(p["pos"][r], np.arange(rows8[i]))
         assert np.all(p["seq"][r] == i)
-        assert p["vbase"][i] % 16 == 0
-        assert np.array_equal(p["vcol"][r], p["vbase"][i] + np.arange(b.lens[i]))
-    assert np.all(np.diff(p["vbase"]) >= b.lens[:-1])                      # V^T columns never overlap
-    # encoder tiles: every row of every question exactly once, <= 64 queries, inside its question
+        assert soff[i] % 8 == 0
+    # encoder tiles: every valid row of every question exactly once, <= 64 queries, inside its question
     cover = np.zeros(p["T"], int)
     for seq, q0, nq, _ in p["tiles"]:
         assert 1 <= nq <= 64 and q0 % 64 == 0 and q0 + nq <= b.lens[seq]
         cover[soff[seq] + q0: soff[seq] + q0 + nq] += 1
-    assert np.all(cover == 1)
+    valid_rows = np.concatenate([np.arange(soff[i], soff[i] + b.lens[i]) for i in range(b.B)])
+    assert np.all(cover[valid_rows] == 1) and cover.sum() == p["valid"]
     # gathered rows: markers in question order, then one CLS row per question
     KT = int(b.nmark.sum())
     assert p["KT"] == KT and p["R"] == KT + b.B
@@ -117,7 +119,7 @@ def test_layout_of_a_pass(host):
         assert 1 <= nq <= 64
         for gi in p["gq"][start:start + nq]:
             seen[gi] += 1
-            assert soff[seq] <= p["grow"][gi] < soff[seq + 1]
+            assert soff[seq] <= p["grow"][gi] < soff[seq] + b.lens[seq]
     assert np.all(seen == 1)
 
 
@@ -129,11 +131,12 @@ def test_pass_splitting(host):
     def greedy(rows, seqs):                  # questions in order while the pass still fits
         out, cur, t = [], [], 0
         for i, L in enumerate(lens):
-            if cur and (t + L > rows or len(cur) == seqs):
+            L8 = (L + 7) // 8 * 8
+            if cur and (t + L8 > rows or len(cur) == seqs):
                 out.append(cur)
                 cur, t = [], 0
             cur.append(i)
-            t += L
+            t += L8
         return out + [cur]
     for rows, seqs in ((640, 3), (400, 512), (320, 2)):
         ps = plan(host, *b.flat(), max_len=320, pass_tokens=rows, max_seqs=seqs)
@@ -142,6 +145,7 @@ def test_pass_splitting(host):
         assert [p["B"] for p in ps] == [len(g) for g in exp]
         assert all(p["T"] <= rows for p in ps)
     assert [p["B"] for p in plan(host, *b.flat(), max_len=320, pass_tokens=640, max_seqs=3)] == [2, 3, 2]
+    assert [p["B"] for p in plan(host, *b.flat(), max_len=320, pass_tokens=320)] == [1, 1, 2, 1, 2]
     ps = plan(host, *b.flat(), max_len=320, max_grows=256)                 # gathered-row cap
     assert all(p["R"] <= 256 for p in ps) and sum(p["B"] for p in ps) == 7
 
