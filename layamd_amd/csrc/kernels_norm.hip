@@ -32,48 +32,65 @@ template <> struct St4<bf16_t> {
   }
 };
 
-template <typename Tin, typename T>
-__global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows,
-                                                   int D, float eps, const float* __restrict__ w,
-                                                   const float* __restrict__ b, const float* __restrict__ addtab,
-                                                   const int* __restrict__ qt, const int* __restrict__ seq, float* y32,  // may alias x
+// Each wave normalises RPW rows; all of their loads are issued before the first reduction so
+// every lane keeps 4*RPW 16-byte loads in flight.
+template <typename Tin, typename T, int RPW, int NCH>
+__global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows, int D,
+                                                   float eps, const float* __restrict__ w, const float* __restrict__ b,
+                                                   const float* __restrict__ addtab, const int* __restrict__ qt,
+                                                   const int* __restrict__ seq, float* y32,  // may alias x
                                                    T* __restrict__ yT) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   const int nc = D >> 2;
-  const size_t src = gather ? (size_t)gather[row] : (size_t)row;
-  const Tin* xr = x + src * D;
-  float4 v[kLnMaxChunks];
-  float s = 0.f;
+  float4 v[RPW][NCH];
+  float s[RPW];
 #pragma unroll
-  for (int j = 0; j < kLnMaxChunks; j++) {
-    const int c = lane + 64 * j;
-    if (c < nc) { v[j] = Ld4<Tin>::at(xr, c); s += (v[j].x + v[j].y) + (v[j].z + v[j].w); }
-  }
-  const float mean = wave_sum(s) / D;
-  float q = 0.f;
+  for (int q = 0; q < RPW; q++) {
+    s[q] = 0.f;
+    const int row = row0 + q;
+    if (row >= rows) continue;
+    const size_t src = gather ? (size_t)gather[row] : (size_t)row;
+    const Tin* xr = x + src * D;
 #pragma unroll
-  for (int j = 0; j < kLnMaxChunks; j++) {
-    const int c = lane + 64 * j;
-    if (c < nc) {
-      const float a = v[j].x - mean, bb = v[j].y - mean, cc = v[j].z - mean, d = v[j].w - mean;
-      q += (a * a + bb * bb) + (cc * cc + d * d);
+    for (int j = 0; j < NCH; j++) {
+      const int c = lane + 64 * j;
+      if (c < nc) v[q][j] = Ld4<Tin>::at(xr, c);
     }
   }
-  const float inv = rsqrtf(wave_sum(q) / D + eps);
-  const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
 #pragma unroll
-  for (int j = 0; j < kLnMaxChunks; j++) {
-    const int c = lane + 64 * j;
-    if (c < nc) {
-      const float4 ww = reinterpret_cast<const float4*>(w)[c];
-      float4 o = make_float4((v[j].x - mean) * inv * ww.x, (v[j].y - mean) * inv * ww.y,
-                             (v[j].z - mean) * inv * ww.z, (v[j].w - mean) * inv * ww.w);
-      if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
-      if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
-      if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
-      if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
+  for (int q = 0; q < RPW; q++)
+#pragma unroll
+    for (int j = 0; j < NCH; j++)
+      if (lane + 64 * j < nc) s[q] += (v[q][j].x + v[q][j].y) + (v[q][j].z + v[q][j].w);
+#pragma unroll
+  for (int q = 0; q < RPW; q++) {
+    const int row = row0 + q;
+    if (row >= rows) break;
+    const float mean = wave_sum(s[q]) / D;
+    float qq = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const int c = lane + 64 * j;
+      if (c < nc) {
+        const float a = v[q][j].x - mean, bb = v[q][j].y - mean, cc = v[q][j].z - mean, d = v[q][j].w - mean;
+        qq += (a * a + bb * bb) + (cc * cc + d * d);
+      }
+    }
+    const float inv = rsqrtf(wave_sum(qq) / D + eps);
+    const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const int c = lane + 64 * j;
+      if (c < nc) {
+        const float4 ww = reinterpret_cast<const float4*>(w)[c];
+        float4 o = make_float4((v[q][j].x - mean) * inv * ww.x, (v[q][j].y - mean) * inv * ww.y,
+                               (v[q][j].z - mean) * inv * ww.z, (v[q][j].w - mean) * inv * ww.w);
+        if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
+        if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
+        if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
+        if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
+      }
     }
   }
 }
@@ -83,8 +100,14 @@ void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float ep
                       const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st) {
   if (D % 4 || D > kLnMaxChunks * 256) { fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D); exit(1); }
   if (rows <= 0) return;
-  hipLaunchKernelGGL((k_layernorm<Tin, T>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
-                     addtab, qt, seq, y32, yT);
+  if (D <= 1024) {
+    constexpr int RPW = 2;
+    hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x, gather,
+                       rows, D, eps, w, b, addtab, qt, seq, y32, yT);
+  } else {
+    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
+                       addtab, qt, seq, y32, yT);
+  }
 }
 
 template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
