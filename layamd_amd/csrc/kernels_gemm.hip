@@ -291,67 +291,110 @@ __device__ __forceinline__ void tile_coords(int bid, int tilesM, int tilesN, int
   tn = r / gs;
 }
 
-// LDS fill by DMA: buffer_load_dwordx4 ... lds writes lane l's 16 bytes to LDS at (M0 base) +
-// 16*l, so each wave instruction fills 64 consecutive chunks = 8 tile rows.  The swizzle is
-// applied on the global side: the lane landing at row r, chunk position c loads global chunk
-// c ^ (r & 7).  Rows past M (or N) lie outside the buffer resource and arrive as zeros.
-template <int ROWS>
-__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rsrc, u32x4_t* lds, int row0, int ld_bytes, int kbyte,
-                                         int wave, int lane) {
-  constexpr int PER_WAVE = ROWS / 32;                  // instructions per wave (8 rows each)
-  const int rl = lane >> 3, cpos = lane & 7;
+// Buffer resource (V#) of a raw byte range: base, stride 0, num_records = bytes (offsets at or past
+// it read as zero without touching memory), dword 3 = the gfx9 raw-buffer format word.
+__device__ __forceinline__ u32x4_t make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  u32x4_t r;
+  r[0] = (uint32_t)v;
+  r[1] = (uint32_t)(v >> 32) & 0xFFFFu;
+  r[2] = bytes;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// One LDS DMA instruction: lane l copies 16 bytes at rsrc + voff + soff to LDS address lds + 16 l.
+// Issued as inline assembly (M0 holds the LDS base; one wait state between the M0 write and the
+// DMA; no compiler-generated code in these kernels reads M0, which gfx9 LDS instructions ignore),
+// so the compiler sees no LDS write and inserts no waits of its own between these fills and the
+// fragment reads: the main loop orders them with explicit vmcnt waits and barriers.  The memory
+// clobber keeps the compiler from moving LDS reads across the fill.
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// LDS fill by DMA: each wave instruction fills 64 consecutive 16-byte chunks = 16 tile rows of
+// one 32-deep K slice (64 bytes per row).  The swizzle is applied on the global side: the lane
+// landing at row r, chunk position c loads global chunk c ^ f(r), f(r) = ((r >> 1) & 3) ^
+// ((r >> 3) & 1).  A fragment read has lane l on row l % 32 at one logical chunk; with 64 banks of
+// 4 bytes each group of 16 lanes then covers 16 distinct 16-byte bank positions ((r & 3) * 4 +
+// (k ^ f(r)) over r = 0..15), and each group of 8 covers 8 of 8 with 32 banks, so the reads are
+// conflict-free.  The per-lane offset (row * ld + swizzled chunk) is fixed over K; the slice's K
+// byte offset goes in the scalar offset.  Rows past M (or N) are out of range by the per-lane
+// offset alone and arrive as zeros; a slice past the last one is fetched through a resource of
+// zero length, so it reads nothing.
+__device__ __forceinline__ uint32_t dma_voff(int row0, int r, int ld_bytes, int lane) {
+  const int cpos = lane & 3;
+  return (uint32_t)(row0 + r) * (uint32_t)ld_bytes + ((uint32_t)(cpos ^ ((r >> 1) & 3) ^ ((r >> 3) & 1)) << 4);
+}
+
+// Fragments of one 16-deep K step: lane l holds 8 consecutive K values (16 bytes) of tile row
+// (row base + 32 i + l % 32), K offset 8 * (l / 32); ks selects the step within the 32-deep slice.
+template <int FM, int FN>
+struct Frags {
+  u32x4_t a[FM], b[FN];
+};
+
+template <int FM, int FN>
+__device__ __forceinline__ void load_frags(Frags<FM, FN>& f, const u32x4_t* As, const u32x4_t* Bs, int arow, int brow,
+                                           int ks, int hi, int sw) {
 #pragma unroll
-  for (int j = 0; j < PER_WAVE; j++) {
-    const int r = (wave * PER_WAVE + j) * 8 + rl;
-    const int voff = (row0 + r) * ld_bytes + ((cpos ^ (r & 7)) << 4);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds + (wave * PER_WAVE + j) * 64),
-                                             16, voff, kbyte, 0, 0);
-  }
+  for (int i = 0; i < FM; i++) f.a[i] = As[(arow + i * 32) * 4 + ((2 * ks + hi) ^ sw)];
+#pragma unroll
+  for (int j = 0; j < FN; j++) f.b[j] = Bs[(brow + j * 32) * 4 + ((2 * ks + hi) ^ sw)];
 }
 
 template <int FM, int FN>
-__device__ __forceinline__ void load_frags(const u32x4_t* As, const u32x4_t* Bs, int arow, int brow, int s, int lane,
-                                           u32x4_t (&af)[FM], u32x4_t (&bf)[FN]) {
-  const int ch = (2 * s + (lane >> 5)) ^ (lane & 7);
-#pragma unroll
-  for (int i = 0; i < FM; i++) af[i] = As[(arow + i * 32) * 8 + ch];
-#pragma unroll
-  for (int j = 0; j < FN; j++) bf[j] = Bs[(brow + j * 32) * 8 + ch];
-}
-
-template <int FM, int FN>
-__device__ __forceinline__ void mma_step(f32x16_t (&acc)[FM][FN], const u32x4_t (&af)[FM], const u32x4_t (&bf)[FN]) {
+__device__ __forceinline__ void mma_frags(f32x16_t (&acc)[FM][FN], const Frags<FM, FN>& f) {
 #pragma unroll
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int j = 0; j < FN; j++)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, af[i]),
-                                                          __builtin_bit_cast(bf16x8_t, bf[j]), acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
+                                                          __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
 }
 
-// one 64-deep K slice from one LDS stage: 4 steps of 16, fragments double-buffered in registers
+// single-fragment and single-MFMA forms of the above, for interleaved issue
 template <int FM, int FN>
-__device__ __forceinline__ void mma_slice(f32x16_t (&acc)[FM][FN], const u32x4_t* As, const u32x4_t* Bs, int arow,
-                                          int brow, int lane) {
-  u32x4_t a0[FM], b0[FN], a1[FM], b1[FN];
-  load_frags<FM, FN>(As, Bs, arow, brow, 0, lane, a0, b0);
-  load_frags<FM, FN>(As, Bs, arow, brow, 1, lane, a1, b1);
-  mma_step<FM, FN>(acc, a0, b0);
-  load_frags<FM, FN>(As, Bs, arow, brow, 2, lane, a0, b0);
-  mma_step<FM, FN>(acc, a1, b1);
-  load_frags<FM, FN>(As, Bs, arow, brow, 3, lane, a1, b1);
-  mma_step<FM, FN>(acc, a0, b0);
-  mma_step<FM, FN>(acc, a1, b1);
+__device__ __forceinline__ void load_frag(Frags<FM, FN>& f, int idx, const u32x4_t* As, const u32x4_t* Bs, int arow,
+                                          int brow, int ks, int hi, int sw) {
+  if (idx < FM) f.a[idx] = As[(arow + idx * 32) * 4 + ((2 * ks + hi) ^ sw)];
+  else f.b[idx - FM] = Bs[(brow + (idx - FM) * 32) * 4 + ((2 * ks + hi) ^ sw)];
 }
+
+template <int FM, int FN>
+__device__ __forceinline__ void mma_one(f32x16_t (&acc)[FM][FN], const Frags<FM, FN>& f, int t) {
+  const int i = t / FN, j = t % FN;
+  acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]), __builtin_bit_cast(bf16x8_t, f.b[j]),
+                                                      acc[i][j], 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0): all but this wave's n most recent vector-memory instructions
+// (here: DMA fills) have completed, and so have all of its LDS reads.  Placed before each barrier:
+// after it, no wave has an LDS read of an older stage in flight.
+#define LAYA_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(n) : "memory")
 
 template <int BM, int BN, int WM, int WN, int EPI, int ACT>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int PER_SLICE = BM / 64 + BN / 64;         // DMA instructions per thread per K slice
   static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
-  __shared__ u32x4_t As0[BM * 8], As1[BM * 8];      // two K stages, separate objects so the
-  __shared__ u32x4_t Bs0[BN * 8], Bs1[BN * 8];      // compiler sees DMA and reads never alias
+  // the epilogue stages each wave's output in one whole stage ((BM + BN) * 64 bytes)
+  static_assert(WTM * (EPI == EPI_GEGLU ? WTN / 2 : WTN) * 2 <= (BM + BN) * 64 && 32 * 64 * 4 <= (BM + BN) * 64,
+                "epilogue staging");
+  // five 32-deep K stages ((BM + BN) * 64 bytes each), separate objects so the compiler sees that
+  // the DMA into one stage and the fragment reads of another never alias
+  struct Stage { u32x4_t a[BM * 4]; u32x4_t b[BN * 4]; };
+  __shared__ Stage S0, S1, S2, S3, S4;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
@@ -360,16 +403,53 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   tile_coords(blockIdx.x, tilesM, tilesN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(a.A), (short)0, (int)((size_t)a.M * a.lda * sizeof(T)), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<void*>(a.W), (short)0, (int)((size_t)a.N * a.ldw * sizeof(T)), 0x00020000);
+  const u32x4_t rA = make_rsrc(a.A, (uint32_t)((size_t)a.M * a.lda * sizeof(T)));
+  const u32x4_t rB = make_rsrc(a.W, (uint32_t)((size_t)a.N * a.ldw * sizeof(T)));
   const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
+
+  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
+  const int nk = a.K / 32;
+  const int sw = ((lane >> 1) & 3) ^ ((lane >> 3) & 1);   // f(row) of fragment rows 32 n + lane % 32
+  constexpr int PA = BM / 64, PB = BN / 64;             // DMA instructions per wave and slice
+  // per-lane offsets of this wave's DMA instructions (fixed over K) and their LDS destinations
+  uint32_t voff[PA + PB];
+#pragma unroll
+  for (int o = 0; o < PA + PB; o++)
+    voff[o] = o < PA ? dma_voff(m0, (wave * PA + o) * 16 + (lane >> 2), lda_b, lane)
+                     : dma_voff(n0, (wave * PB + o - PA) * 16 + (lane >> 2), ldw_b, lane);
+  const uint32_t wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
+  const uint32_t wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
+  const u32x4_t rNone = make_rsrc(a.A, 0u);               // zero length: every offset out of range
+  // instruction o (A rows first, then W rows) of slice kt into stage S
+  auto dma_op = [&](int o, Stage& S, int kt) {
+    const bool live = kt < nk;
+    if (o < PA) dma16(live ? rA : rNone, lds_addr(S.a) + wsa + o * 1024, voff[o], (uint32_t)kt * 64u);
+    else dma16(live ? rB : rNone, lds_addr(S.b) + wsb + (o - PA) * 1024, voff[o], (uint32_t)kt * 64u);
+  };
+  auto dma = [&](int kt, Stage& S) {
+#pragma unroll
+    for (int o = 0; o < PA + PB; o++) dma_op(o, S, kt);
+  };
+  // Pipeline: slice s is fetched into stage s % 5 four steps ahead.  Step kt multiplies the two
+  // 16-deep halves of slice kt from registers (F0, F1) while loading the next half: F1 (slice kt,
+  // second half) during the first, F0 (slice kt + 1, first half) during the second.  Between the
+  // halves each wave waits for its own part of slice kt + 1 (two later slices may stay in flight),
+  // then the barrier makes slice kt + 1 visible to all waves and frees stage (kt - 1) % 5, whose
+  // last reads (F1 of slice kt - 1) were consumed before every wave reached this point; the refill
+  // of that stage with slice kt + 4 is issued right after it.  Every step issues the same number of
+  // DMA instructions (past the last slice they are out of range), so the wait count is constant.
+  // The loop body starts after a step's barrier: (refill, F0 <- next slice, F1 MFMAs) | (F1 <- next
+  // slice, F0 MFMAs, wait, barrier).
+  dma(0, S0);
+  dma(1, S1);
+  dma(2, S2);
+  dma(3, S3);
 
   f32x16_t acc[FM][FN];
   if constexpr (EPI == EPI_RESID) {
     // the residual update X += A W^T + b starts the accumulators at X (rows/cols outside X read 0),
-    // so the epilogue issues no global load after its first store
+    // so the epilogue issues no global load after its first store.  These loads come after the
+    // DMA fills, so the wait for them (before the first MFMA) also covers the prologue slices.
     const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
         a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
     const int r0 = m0 + wm * WTM + 4 * hi, c0 = n0 + wn * WTN + l32;
@@ -392,27 +472,66 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
         for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
   }
 
-  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
-  const int nk = a.K / 64;
-  dma_tile<BM>(rA, As0, m0, lda_b, 0, wave, lane);
-  dma_tile<BN>(rB, Bs0, n0, ldw_b, 0, wave, lane);
-  __syncthreads();
-  // pairs of K slices with both stages unconditional (keeps the accumulators in place), then an
-  // odd tail from stage 0
-  int kt = 0;
-  for (; kt + 2 <= nk; kt += 2) {
-    dma_tile<BM>(rA, As1, m0, lda_b, (kt + 1) * 128, wave, lane);
-    dma_tile<BN>(rB, Bs1, n0, ldw_b, (kt + 1) * 128, wave, lane);
-    mma_slice<FM, FN>(acc, As0, Bs0, arow, brow, lane);
-    __syncthreads();
-    if (kt + 2 < nk) {
-      dma_tile<BM>(rA, As0, m0, lda_b, (kt + 2) * 128, wave, lane);
-      dma_tile<BN>(rB, Bs0, n0, ldw_b, (kt + 2) * 128, wave, lane);
-    }
-    mma_slice<FM, FN>(acc, As1, Bs1, arow, brow, lane);
-    __syncthreads();
+  Frags<FM, FN> F0, F1;
+  LAYA_WAIT_VMCNT(3 * PER_SLICE);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  load_frags(F0, S0.a, S0.b, arow, brow, 0, hi, sw);
+  load_frags(F1, S0.a, S0.b, arow, brow, 1, hi, sw);
+  mma_frags(acc, F0);
+  LAYA_WAIT_VMCNT(2 * PER_SLICE);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // one step from the barrier of step kt - 1 to that of step kt: refill stage SR with slice
+  // kt + 3, F0 <- slice kt (SN) first half, MFMAs of F1 (slice kt - 1, second half), F1 <- slice kt
+  // second half, MFMAs of F0, wait for slice kt + 1, barrier.
+// With one or two waves per SIMD the MFMA pipe idles whenever a wave issues anything else, so the
+// DMA instructions and the fragment loads of the next half are spread between the MFMAs of the
+// current one (first half: DMA then F0 loads; second half: F1 loads), each MFMA followed by its
+// share, fixed by scheduling fences.
+  constexpr int NMM = FM * FN, E1 = PA + PB + FM + FN, E2 = FM + FN;
+#define LAYA_GEMM_STEP(SN, SR)                                                            \
+  {                                                                                       \
+    _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
+      mma_one(acc, F1, t);                                                                \
+      _Pragma("unroll") for (int o = t * E1 / NMM; o < (t + 1) * E1 / NMM; o++) {        \
+        if (o < PA + PB) dma_op(o, SR, kt + 4);                                           \
+        else load_frag(F0, o - PA - PB, SN.a, SN.b, arow, brow, 0, hi, sw);               \
+      }                                                                                   \
+      __builtin_amdgcn_sched_barrier(0);                                                  \
+    }                                                                                     \
+    ++kt;                                                                                 \
+    _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
+      mma_one(acc, F0, t);                                                                \
+      _Pragma("unroll") for (int o = t * E2 / NMM; o < (t + 1) * E2 / NMM; o++)          \
+        load_frag(F1, o, SN.a, SN.b, arow, brow, 1, hi, sw);                              \
+      __builtin_amdgcn_sched_barrier(0);                                                  \
+    }                                                                                     \
+    LAYA_WAIT_VMCNT(2 * PER_SLICE);                                                       \
+    __builtin_amdgcn_s_barrier();                                                         \
+    asm volatile("" ::: "memory");                                                        \
   }
-  if (kt < nk) mma_slice<FM, FN>(acc, As0, Bs0, arow, brow, lane);
+  int kt = 0;                              // slice whose first half has been multiplied
+  for (; kt + 6 <= nk;) {                  // five whole steps, the last one loading slice kt + 5
+    LAYA_GEMM_STEP(S1, S4)
+    LAYA_GEMM_STEP(S2, S0)
+    LAYA_GEMM_STEP(S3, S1)
+    LAYA_GEMM_STEP(S4, S2)
+    LAYA_GEMM_STEP(S0, S3)
+  }
+  if (kt + 1 < nk) {                       // at most four whole steps remain
+    LAYA_GEMM_STEP(S1, S4)
+    if (kt + 1 < nk) {
+      LAYA_GEMM_STEP(S2, S0)
+      if (kt + 1 < nk) {
+        LAYA_GEMM_STEP(S3, S1)
+        if (kt + 1 < nk) LAYA_GEMM_STEP(S4, S2)
+      }
+    }
+  }
+  mma_frags(acc, F1);                      // second half of the last slice
+#undef LAYA_GEMM_STEP
+  LAYA_WAIT_VMCNT(0);                      // the out-of-range refills of the last steps
 
   // ---------------- epilogue ----------------
   // On gfx9 vmcnt counts stores as well as loads, so a global load issued after a store waits for
@@ -432,7 +551,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   };
   if constexpr (EPI == EPI_RESID) {
     // per 32 x 64 block through an fp32 scratch of 8 KiB per wave; no loads in the loop
-    float* scr = reinterpret_cast<float*>(wave < 2 ? As0 : As1) + (wave & 1) * 2048;
+    float* scr = reinterpret_cast<float*>(wave == 0 ? &S0 : wave == 1 ? &S1 : wave == 2 ? &S2 : &S3);
     auto sidx = [](int r, int c) { return r * 64 + ((((c >> 2) ^ (r & 15))) << 2) + (c & 3); };
     float bias[FN];
 #pragma unroll
@@ -467,7 +586,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     // phase 1: the wave's finished tile -> LDS as bf16, [WTM][OW] with 16-byte chunks swizzled by row
     constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;     // output columns of the wave tile
     constexpr int CPRW = OW / 8;                             // 16-byte chunks per row
-    bf16_t* wt = reinterpret_cast<bf16_t*>(wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? Bs0 : Bs1);
+    bf16_t* wt = reinterpret_cast<bf16_t*>(wave == 0 ? &S0 : wave == 1 ? &S1 : wave == 2 ? &S2 : &S3);
     auto oidx = [](int r, int c) { return r * OW + ((((c >> 3) ^ (r & 7)) & (CPRW - 1)) << 3) + (c & 7); };
     const bool odd = lane & 1;
     // element e of a 32x32 block is row 8*(e/4) + 4*hi + e%4: elements (e, e+1), e even, are rows
@@ -487,8 +606,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           const float bx = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, by = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
 #pragma unroll
           for (int e = 0; e < 16; e += 2)
-            put(i, e, jp * 16, gelu_erf(acc[i][jp][e] + bx) * (acc[i][jp + 1][e] + by),
-                gelu_erf(acc[i][jp][e + 1] + bx) * (acc[i][jp + 1][e + 1] + by));
+            put(i, e, jp * 16, gelu_erf_as(acc[i][jp][e] + bx) * (acc[i][jp + 1][e] + by),
+                gelu_erf_as(acc[i][jp][e + 1] + bx) * (acc[i][jp + 1][e + 1] + by));
         } else if constexpr (EPI == EPI_QKV) {
           const bool ok = c0 < a.N;
           const float b0 = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, b1 = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
@@ -523,7 +642,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
             auto f = [&](float v) {
               v += bb;
               if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
-              if constexpr (ACT == ACT_GELU) v = gelu_erf(v);
+              if constexpr (ACT == ACT_GELU) v = gelu_erf_as(v);
               return v;
             };
 #pragma unroll

@@ -65,7 +65,8 @@ def golden_flat_logits(c):
 
 # ---------------------------------------------------------------- GEMM kernel vs torch fp32
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
-@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (513, 1024, 2624)])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (200, 256, 320),
+                                   (513, 1024, 2624)])
 def test_gemm_vs_torch(dtype, M, N, K):
     import torch
     lib = le.load_library()
