@@ -381,133 +381,88 @@ __device__ __forceinline__ void mma_one(f32x16_t (&acc)[FM][FN], const Frags<FM,
 // after it, no wave has an LDS read of an older stage in flight.
 #define LAYA_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(n) : "memory")
 
-template <int BM, int BN, int WM, int WN, int EPI, int ACT>
-__global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
-  using T = bf16_t;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int PER_SLICE = BM / 64 + BN / 64;         // DMA instructions per thread per K slice
-  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
-  // the epilogue stages each wave's output in one whole stage ((BM + BN) * 64 bytes)
-  static_assert(WTM * (EPI == EPI_GEGLU ? WTN / 2 : WTN) * 2 <= (BM + BN) * 64 && 32 * 64 * 4 <= (BM + BN) * 64,
-                "epilogue staging");
-  // five 32-deep K stages ((BM + BN) * 64 bytes each), separate objects so the compiler sees that
-  // the DMA into one stage and the fragment reads of another never alias
-  struct Stage { u32x4_t a[BM * 4]; u32x4_t b[BN * 4]; };
-  __shared__ Stage S0, S1, S2, S3, S4;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
-  const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
-  int tm, tn;
-  tile_coords(blockIdx.x, tilesM, tilesN, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  const u32x4_t rA = make_rsrc(a.A, (uint32_t)((size_t)a.M * a.lda * sizeof(T)));
-  const u32x4_t rB = make_rsrc(a.W, (uint32_t)((size_t)a.N * a.ldw * sizeof(T)));
-  const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
-
-  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
-  const int nk = a.K / 32;
-  const int sw = ((lane >> 1) & 3) ^ ((lane >> 3) & 1);   // f(row) of fragment rows 32 n + lane % 32
-  constexpr int PA = BM / 64, PB = BN / 64;             // DMA instructions per wave and slice
-  // per-lane offsets of this wave's DMA instructions (fixed over K) and their LDS destinations
+// DMA plan of one workgroup: resources of A and W (and one of zero length for slices past the
+// last), the per-lane offsets of this wave's PA + PB instructions per slice (A rows, then W rows)
+// and the wave's byte offset inside each stage part.
+template <int PA, int PB>
+struct XlDma {
+  u32x4_t rA, rB, rNone;
   uint32_t voff[PA + PB];
-#pragma unroll
-  for (int o = 0; o < PA + PB; o++)
-    voff[o] = o < PA ? dma_voff(m0, (wave * PA + o) * 16 + (lane >> 2), lda_b, lane)
-                     : dma_voff(n0, (wave * PB + o - PA) * 16 + (lane >> 2), ldw_b, lane);
-  const uint32_t wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
-  const uint32_t wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
-  const u32x4_t rNone = make_rsrc(a.A, 0u);               // zero length: every offset out of range
-  // instruction o (A rows first, then W rows) of slice kt into stage S
-  auto dma_op = [&](int o, Stage& S, int kt) {
+  uint32_t wsa, wsb;
+  int nk;
+  template <class ST>
+  __device__ __forceinline__ void op(int o, ST& S, int kt) const {
     const bool live = kt < nk;
     if (o < PA) dma16(live ? rA : rNone, lds_addr(S.a) + wsa + o * 1024, voff[o], (uint32_t)kt * 64u);
     else dma16(live ? rB : rNone, lds_addr(S.b) + wsb + (o - PA) * 1024, voff[o], (uint32_t)kt * 64u);
-  };
-  auto dma = [&](int kt, Stage& S) {
-#pragma unroll
-    for (int o = 0; o < PA + PB; o++) dma_op(o, S, kt);
-  };
-  // Pipeline: slice s is fetched into stage s % 5 four steps ahead.  Step kt multiplies the two
-  // 16-deep halves of slice kt from registers (F0, F1) while loading the next half: F1 (slice kt,
-  // second half) during the first, F0 (slice kt + 1, first half) during the second.  Between the
-  // halves each wave waits for its own part of slice kt + 1 (two later slices may stay in flight),
-  // then the barrier makes slice kt + 1 visible to all waves and frees stage (kt - 1) % 5, whose
-  // last reads (F1 of slice kt - 1) were consumed before every wave reached this point; the refill
-  // of that stage with slice kt + 4 is issued right after it.  Every step issues the same number of
-  // DMA instructions (past the last slice they are out of range), so the wait count is constant.
-  // The loop body starts after a step's barrier: (refill, F0 <- next slice, F1 MFMAs) | (F1 <- next
-  // slice, F0 MFMAs, wait, barrier).
-  dma(0, S0);
-  dma(1, S1);
-  dma(2, S2);
-  dma(3, S3);
-
-  f32x16_t acc[FM][FN];
-  if constexpr (EPI == EPI_RESID) {
-    // the residual update X += A W^T + b starts the accumulators at X (rows/cols outside X read 0),
-    // so the epilogue issues no global load after its first store.  These loads come after the
-    // DMA fills, so the wait for them (before the first MFMA) also covers the prologue slices.
-    const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
-        a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
-    const int r0 = m0 + wm * WTM + 4 * hi, c0 = n0 + wn * WTN + l32;
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int row = r0 + i * 32 + 8 * (e >> 2) + (e & 3), col = c0 + j * 32;
-          const int off = col < a.N ? (row * a.ldx + col) * 4 : 0x7FFFFFF0;
-          acc[i][j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rX, off, 0, 0));
-        }
-  } else {
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
   }
+  template <class ST>
+  __device__ __forceinline__ void slice(ST& S, int kt) const {
+#pragma unroll
+    for (int o = 0; o < PA + PB; o++) op(o, S, kt);
+  }
+};
 
+// acc[i][j] += A block i . W block j^T (SWAP: the transposed product W block j . A block i^T,
+// whose accumulator layout gives each lane 4 consecutive output columns of one row)
+template <bool SWAP, int FM, int FN>
+__device__ __forceinline__ void mma_one_x(f32x16_t (&acc)[FM][FN], const Frags<FM, FN>& f, int t) {
+  const int i = t / FN, j = t % FN;
+  if constexpr (SWAP)
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.b[j]),
+                                                        __builtin_bit_cast(bf16x8_t, f.a[i]), acc[i][j], 0, 0, 0);
+  else
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
+                                                        __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
+}
+
+// The K loop of one tile.  Slice s (32 deep) is fetched into stage s % 5 four steps ahead; slices
+// 0..3 were issued by the caller.  Step kt multiplies the two 16-deep halves of slice kt from
+// registers (F0, F1) while loading the next half: F1 (slice kt, second half) during the first, F0
+// (slice kt + 1, first half) during the second.  Between the halves each wave waits for its own
+// part of slice kt + 1 (two later slices may stay in flight), then the barrier makes slice kt + 1
+// visible to all waves and frees stage (kt - 1) % 5, whose last reads (F1 of slice kt - 1) were
+// consumed before every wave reached it; the refill of that stage with slice kt + 4 follows.  Every
+// step issues the same number of DMA instructions (past the last slice they read nothing), so the
+// wait count is constant.  With one or two waves per SIMD the MFMA pipe idles whenever a wave issues
+// anything else, so the DMA instructions and the fragment loads of the next half are spread between
+// the MFMAs of the current one (first half: DMA then F0 loads; second half: F1 loads), each MFMA
+// followed by its share, fixed by scheduling fences.
+template <bool SWAP, int FM, int FN, int PA, int PB, class ST>
+__device__ __forceinline__ void xl_k_loop(f32x16_t (&acc)[FM][FN], ST& S0, ST& S1, ST& S2, ST& S3, ST& S4,
+                                          const XlDma<PA, PB>& d, int arow, int brow, int hi, int sw) {
+  constexpr int PS = PA + PB, NMM = FM * FN, E1 = PA + PB + FM + FN, E2 = FM + FN;
+  const int nk = d.nk;
   Frags<FM, FN> F0, F1;
-  LAYA_WAIT_VMCNT(3 * PER_SLICE);
+  LAYA_WAIT_VMCNT(3 * PS);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   load_frags(F0, S0.a, S0.b, arow, brow, 0, hi, sw);
   load_frags(F1, S0.a, S0.b, arow, brow, 1, hi, sw);
-  mma_frags(acc, F0);
-  LAYA_WAIT_VMCNT(2 * PER_SLICE);
+#pragma unroll
+  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F0, t);
+  LAYA_WAIT_VMCNT(2 * PS);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  // one step from the barrier of step kt - 1 to that of step kt: refill stage SR with slice
-  // kt + 3, F0 <- slice kt (SN) first half, MFMAs of F1 (slice kt - 1, second half), F1 <- slice kt
-  // second half, MFMAs of F0, wait for slice kt + 1, barrier.
-// With one or two waves per SIMD the MFMA pipe idles whenever a wave issues anything else, so the
-// DMA instructions and the fragment loads of the next half are spread between the MFMAs of the
-// current one (first half: DMA then F0 loads; second half: F1 loads), each MFMA followed by its
-// share, fixed by scheduling fences.
-  constexpr int NMM = FM * FN, E1 = PA + PB + FM + FN, E2 = FM + FN;
+  // one step, from the barrier that published slice kt to the one that publishes slice kt + 1
 #define LAYA_GEMM_STEP(SN, SR)                                                            \
   {                                                                                       \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
-      mma_one(acc, F1, t);                                                                \
+      mma_one_x<SWAP>(acc, F1, t);                                                        \
       _Pragma("unroll") for (int o = t * E1 / NMM; o < (t + 1) * E1 / NMM; o++) {        \
-        if (o < PA + PB) dma_op(o, SR, kt + 4);                                           \
+        if (o < PA + PB) d.op(o, SR, kt + 4);                                             \
         else load_frag(F0, o - PA - PB, SN.a, SN.b, arow, brow, 0, hi, sw);               \
       }                                                                                   \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
     ++kt;                                                                                 \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
-      mma_one(acc, F0, t);                                                                \
+      mma_one_x<SWAP>(acc, F0, t);                                                        \
       _Pragma("unroll") for (int o = t * E2 / NMM; o < (t + 1) * E2 / NMM; o++)          \
         load_frag(F1, o, SN.a, SN.b, arow, brow, 1, hi, sw);                              \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
-    LAYA_WAIT_VMCNT(2 * PER_SLICE);                                                       \
+    LAYA_WAIT_VMCNT(2 * PS);                                                              \
     __builtin_amdgcn_s_barrier();                                                         \
     asm volatile("" ::: "memory");                                                        \
   }
@@ -529,177 +484,310 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       }
     }
   }
-  mma_frags(acc, F1);                      // second half of the last slice
 #undef LAYA_GEMM_STEP
-  LAYA_WAIT_VMCNT(0);                      // the out-of-range refills of the last steps
+#pragma unroll
+  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);   // second half of the last slice
+  LAYA_WAIT_VMCNT(0);                                            // the refills past the last slice
+}
+
+template <int BM, int BN, int WM, int WN, int EPI, int ACT>
+__global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
+  using T = bf16_t;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int PA = BM / 64, PB = BN / 64;              // DMA instructions per wave and slice
+  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0, "tile");
+  // five 32-deep K stages ((BM + BN) * 64 bytes each), separate objects so the compiler sees that
+  // the DMA into one stage and the fragment reads of another never alias
+  struct Stage { u32x4_t a[BM * 4]; u32x4_t b[BN * 4]; };
+  __shared__ Stage S0, S1, S2, S3, S4;
+  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BM + BN) * 64, "RoPE tables: one stage each for cos and sin");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
+  const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
+  int tm, tn;
+  tile_coords(blockIdx.x, tilesM, tilesN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int D = a.H * a.HD;
+  // all tiles use the transposed product except the V columns of the QKV projection, which are
+  // stored transposed themselves (V^T) and keep the direct one
+  const bool swap = EPI == EPI_QKV ? n0 < 2 * D : true;
+
+  XlDma<PA, PB> dm;
+  dm.rA = make_rsrc(a.A, (uint32_t)((size_t)a.M * a.lda * sizeof(T)));
+  dm.rB = make_rsrc(a.W, (uint32_t)((size_t)a.N * a.ldw * sizeof(T)));
+  dm.rNone = make_rsrc(a.A, 0u);           // zero length: every offset out of range
+  const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
+#pragma unroll
+  for (int o = 0; o < PA + PB; o++)
+    dm.voff[o] = o < PA ? dma_voff(m0, (wave * PA + o) * 16 + (lane >> 2), lda_b, lane)
+                        : dma_voff(n0, (wave * PB + o - PA) * 16 + (lane >> 2), ldw_b, lane);
+  dm.wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
+  dm.wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
+  dm.nk = a.K / 32;
+  dm.slice(S0, 0);
+  dm.slice(S1, 1);
+  dm.slice(S2, 2);
+  dm.slice(S3, 3);
+
+  // Output coordinates.  Transposed product: lane holds, for block (i, j) and element e, output row
+  // rbase + 32 i + lane % 32 and columns cbase + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4, i.e. four
+  // consecutive columns per e / 4.  Direct product: rows rbase + 32 i + 8 (e / 4) + 4 (lane / 32) +
+  // e % 4 (four consecutive rows per e / 4) and column cbase + 32 j + lane % 32.
+  const int rbase = m0 + wm * WTM, cbase = n0 + wn * WTN;
+  f32x16_t acc[FM][FN];
+  if constexpr (EPI == EPI_RESID) {
+    // the residual update X += A W^T + b starts the accumulators at X (16-byte loads of 4 columns;
+    // rows past M read 0, columns past N are never stored), so the epilogue loads nothing after its
+    // first store.  These loads come after the DMA fills, so the wait for them (before the first
+    // MFMA) also covers the prologue slices.
+    const __amdgpu_buffer_rsrc_t rX =
+        __builtin_amdgcn_make_buffer_rsrc(a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint32_t off = ((uint32_t)(rbase + i * 32 + l32) * (uint32_t)a.ldx + (uint32_t)(cbase + j * 32 + 8 * g + 4 * hi)) * 4u;
+          // reinterpret the whole 16 bytes as floats (a bit_cast of one vector component is
+          // miscompiled by this compiler: it reads component 0)
+          const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
+#pragma unroll
+          for (int u = 0; u < 4; u++) acc[i][j][4 * g + u] = x[u];
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+  }
+
+  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
+  const int sw = ((lane >> 1) & 3) ^ ((lane >> 3) & 1);   // f(row) of fragment rows 32 n + lane % 32
+  if (swap) xl_k_loop<true>(acc, S0, S1, S2, S3, S4, dm, arow, brow, hi, sw);
+  else xl_k_loop<false>(acc, S0, S1, S2, S3, S4, dm, arow, brow, hi, sw);
 
   // ---------------- epilogue ----------------
-  // On gfx9 vmcnt counts stores as well as loads, so a global load issued after a store waits for
-  // that store.  The epilogue therefore loads everything it needs (bias, positions, RoPE tables)
-  // before its first store: residual updates started their accumulators at X above and only add
-  // a preloaded bias; the other epilogues finish every value of the wave's tile into LDS first
-  // (bf16, the K stages are idle) and then stream it out as 16-byte row segments.
-  __syncthreads();
-  const int rbase = m0 + wm * WTM, cbase = n0 + wn * WTN;
-  auto pack8 = [](float4 x, float4 y) {
-    u32x4_t u;
-    u[0] = (uint32_t)f2bf(x.x) | ((uint32_t)f2bf(x.y) << 16);
-    u[1] = (uint32_t)f2bf(x.z) | ((uint32_t)f2bf(x.w) << 16);
-    u[2] = (uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16);
-    u[3] = (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16);
-    return u;
-  };
-  if constexpr (EPI == EPI_RESID) {
-    // per 32 x 64 block through an fp32 scratch of 8 KiB per wave; no loads in the loop
-    float* scr = reinterpret_cast<float*>(wave == 0 ? &S0 : wave == 1 ? &S1 : wave == 2 ? &S2 : &S3);
-    auto sidx = [](int r, int c) { return r * 64 + ((((c >> 2) ^ (r & 15))) << 2) + (c & 3); };
-    float bias[FN];
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-      const int col = cbase + j * 32 + l32;
-      bias[j] = (a.bias && col < a.N) ? a.bias[col] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-#pragma unroll
-      for (int jp = 0; jp < FN; jp += 2) {
-        const int row0 = rbase + i * 32, c0 = cbase + jp * 32;
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) scr[sidx(8 * (e >> 2) + 4 * hi + (e & 3), 32 * b + l32)] = acc[i][jp + b][e] + bias[jp + b];
-        __builtin_amdgcn_s_waitcnt(0xC07F);                 // lgkmcnt(0): this wave's LDS writes are done
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-          const int item = lane + 64 * it, r = item >> 4, q = item & 15;
-          const int row = row0 + r, col = c0 + 4 * q;
-          if (row < a.M && col < a.N)
-            *reinterpret_cast<float4*>(a.X + (size_t)row * a.ldx + col) =
-                *reinterpret_cast<const float4*>(scr + r * 64 + ((q ^ (r & 15)) << 2));
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-  } else {
-    // phase 1: the wave's finished tile -> LDS as bf16, [WTM][OW] with 16-byte chunks swizzled by row
-    constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;     // output columns of the wave tile
-    constexpr int CPRW = OW / 8;                             // 16-byte chunks per row
-    bf16_t* wt = reinterpret_cast<bf16_t*>(wave == 0 ? &S0 : wave == 1 ? &S1 : wave == 2 ? &S2 : &S3);
-    auto oidx = [](int r, int c) { return r * OW + ((((c >> 3) ^ (r & 7)) & (CPRW - 1)) << 3) + (c & 7); };
-    const bool odd = lane & 1;
-    // element e of a 32x32 block is row 8*(e/4) + 4*hi + e%4: elements (e, e+1), e even, are rows
-    // (r, r+1) of column l32; after the pair swap this lane writes 4 bytes at (r + odd, l32 & ~1)
-    auto put = [&](int i, int e, int cblk, float ve, float ve1) {
-      const int r = i * 32 + 8 * (e >> 2) + 4 * hi + (e & 3) + (odd ? 1 : 0);
-      *reinterpret_cast<uint32_t*>(wt + oidx(r, cblk + (l32 & ~1))) = pair_rows_to_cols(ve, ve1, odd);
-    };
-    const int D = a.H * a.HD;
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-#pragma unroll
-      for (int jp = 0; jp < FN; jp += 2) {
-        const int c0 = cbase + jp * 32;
-        if constexpr (EPI == EPI_GEGLU) {
-          const bool ok = c0 < a.N;
-          const float bx = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, by = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
-#pragma unroll
-          for (int e = 0; e < 16; e += 2)
-            put(i, e, jp * 16, gelu_erf_as(acc[i][jp][e] + bx) * (acc[i][jp + 1][e] + by),
-                gelu_erf_as(acc[i][jp][e + 1] + bx) * (acc[i][jp + 1][e + 1] + by));
-        } else if constexpr (EPI == EPI_QKV) {
-          const bool ok = c0 < a.N;
-          const float b0 = (a.bias && ok) ? a.bias[c0 + l32] : 0.f, b1 = (a.bias && ok) ? a.bias[c0 + 32 + l32] : 0.f;
-          if (a.rope_cos && c0 < 2 * D) {
-#pragma unroll
-            for (int e = 0; e < 16; e += 2) {
-              float o1[2], o2[2];
-#pragma unroll
-              for (int u = 0; u < 2; u++) {
-                const int r = i * 32 + 8 * ((e + u) >> 2) + 4 * hi + ((e + u) & 3);
-                const int p = a.pos[min(rbase + r, a.M - 1)];
-                const float c = a.rope_cos[p * 32 + l32], sn = a.rope_sin[p * 32 + l32];
-                const float x1 = acc[i][jp][e + u] + b0, x2 = acc[i][jp + 1][e + u] + b1;
-                o1[u] = x1 * c - x2 * sn;
-                o2[u] = x2 * c + x1 * sn;
-              }
-              put(i, e, jp * 32, o1[0], o1[1]);
-              put(i, e, jp * 32 + 32, o2[0], o2[1]);
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 16; e += 2) {
-              put(i, e, jp * 32, acc[i][jp][e] + b0, acc[i][jp][e + 1] + b0);
-              put(i, e, jp * 32 + 32, acc[i][jp + 1][e] + b1, acc[i][jp + 1][e + 1] + b1);
-            }
-          }
-        } else {  // EPI_STORE
-#pragma unroll
-          for (int b = 0; b < 2; b++) {
-            const int col = c0 + 32 * b + l32;
-            const float bb = (a.bias && col < a.N) ? a.bias[col] : 0.f;
-            auto f = [&](float v) {
-              v += bb;
-              if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
-              if constexpr (ACT == ACT_GELU) v = gelu_erf_as(v);
-              return v;
-            };
-#pragma unroll
-            for (int e = 0; e < 16; e += 2) put(i, e, (jp + b) * 32, f(acc[i][jp + b][e]), f(acc[i][jp + b][e + 1]));
-          }
-        }
-      }
-    }
+  // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
+  // writes the block (bias, activation, GeGLU, RoPE applied in registers) into its quarter of stage
+  // 4 as rows of 16-byte chunks, swizzled by row, then streams whole rows out with 16-byte stores
+  // (full cache lines).  Stages 0-3 stay free (they hold the RoPE tables for the QKV projection).
+  // All global loads are issued before the first store: on gfx9 vmcnt counts stores too, so a load
+  // issued after a store would wait for it.
+  __syncthreads();                                        // every wave is done with the K stages
+  constexpr int SB = (int)(sizeof(Stage) / 4);             // staging bytes per wave
+  char* stg = reinterpret_cast<char*>(&S4) + wave * SB;
+  auto sync_wave = [] {                                   // this wave's LDS writes are visible to it
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
-    // phase 2: stores only
-    if constexpr (EPI == EPI_QKV) {
+  };
+  // byte offset of 16-byte chunk q of staged row r (cpr chunks per row, a power of two)
+  auto sidx = [](int r, int q, int cpr) { return (r * cpr + (q ^ (r & (cpr - 1)))) * 16; };
+  // four bf16 values at staged row r, columns c..c+3 (c % 4 == 0)
+  auto put8 = [&](int r, int c, int cpr, float v0, float v1, float v2, float v3) {
+    uint2 u;
+    u.x = pk_bf16(v0, v1);
+    u.y = pk_bf16(v2, v3);
+    *reinterpret_cast<uint2*>(stg + sidx(r, c >> 3, cpr) + ((c >> 2) & 1) * 8) = u;
+  };
+  // streams 32 staged rows of cpr chunks: row r goes to row_ptr(r) (null: skipped), chunks q < nq
+  auto flush = [&](int cpr, auto&& row_ptr, int nq) {
+    sync_wave();
 #pragma unroll
-      for (int hb = 0; hb < WTN / 64; hb++) {                // one 64-column head block at a time
-        const int c0 = cbase + hb * 64;
-        if (c0 >= a.N) break;
-        const int sec = c0 / D, h = (c0 % D) / a.HD;
-        if (sec == 2) {                                      // V^T: 8 consecutive rows of one column
-          T* vt = reinterpret_cast<T*>(a.Vt) + (size_t)h * a.HD * a.ldv;
+    for (int it = 0; it < 32 * cpr / 64; it++) {
+      const int item = lane + 64 * it, r = item / cpr, q = item % cpr;
+      char* p = row_ptr(r);
+      if (p != nullptr && q < nq)
+        *reinterpret_cast<u32x4_t*>(p + q * 16) = *reinterpret_cast<const u32x4_t*>(stg + sidx(r, q, cpr));
+    }
+    sync_wave();
+  };
+  auto bias4 = [&](int n) -> float4 {
+    return (a.bias && n < a.N) ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto nchunks = [](int valid_elems, int per_chunk, int cpr) { return max(0, min(cpr, (valid_elems + per_chunk - 1) / per_chunk)); };
+  // widest power-of-two column count <= cap that divides w
+  constexpr auto fitw = [](int w, int cap) { int c = w; while (c > cap) c /= 2; return c; };
+
+  if constexpr (EPI == EPI_RESID) {
+    // fp32: blocks of 32 rows x CW columns
+    constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
+    float4 bb[FN][4];
 #pragma unroll
-          for (int it = 0; it < WTM / 8; it++) {
-            const int item = lane + 64 * it, c = item >> (WTM == 128 ? 4 : 3), rg = item & (WTM / 8 - 1);
-            const int row = rbase + 8 * rg;
-            if (row >= a.M) continue;
-            uint32_t u[4];
+    for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int t = 0; t < 4; t++)
-              u[t] = (uint32_t)wt[oidx(8 * rg + 2 * t, hb * 64 + c)] | ((uint32_t)wt[oidx(8 * rg + 2 * t + 1, hb * 64 + c)] << 16);
-            T* dst = vt + (size_t)c * a.ldv + row;
-            if (row + 7 < a.M) {
-              *reinterpret_cast<u32x4_t*>(dst) = (u32x4_t){u[0], u[1], u[2], u[3]};
-            } else {
-              for (int t = 0; t < 8 && row + t < a.M; t++) dst[t] = (bf16_t)(u[t >> 1] >> (16 * (t & 1)));
-            }
+      for (int g = 0; g < 4; g++) bb[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int cp = 0; cp < WTN / CW; cp++) {
+#pragma unroll
+        for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            float4 v;
+            v.x = acc[i][j][4 * g + 0] + bb[j][g].x;
+            v.y = acc[i][j][4 * g + 1] + bb[j][g].y;
+            v.z = acc[i][j][4 * g + 2] + bb[j][g].z;
+            v.w = acc[i][j][4 * g + 3] + bb[j][g].w;
+            *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
           }
+        const int c0 = cbase + cp * CW;
+        flush(CPR, [&](int r) -> char* {
+          const int m = rbase + i * 32 + r;
+          return m < a.M ? reinterpret_cast<char*>(a.X + (size_t)m * a.ldx + c0) : nullptr;
+        }, nchunks(a.N - c0, 4, CPR));
+      }
+  } else if constexpr (EPI == EPI_STORE || EPI == EPI_GEGLU) {
+    // bf16 rows of OW output columns, blocks of 32 rows x CW columns
+    constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;
+    constexpr int CW = fitw(OW, SB / 64), CPR = CW / 8;
+    const int ocol = EPI == EPI_GEGLU ? cbase / 2 : cbase, ncol = EPI == EPI_GEGLU ? a.N / 2 : a.N;
+    // bias per (column block, e / 4): input and gate parts for GeGLU
+    float4 bx[FN][4];
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+    auto f = [](float v) {
+      if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
+      if constexpr (ACT == ACT_GELU) v = gelu_erf_as(v);
+      return v;
+    };
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int cp = 0; cp < OW / CW; cp++) {
+        if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+          for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(acc[i][j][4 * g + 0] + bx[j][g].x),
+                   f(acc[i][j][4 * g + 1] + bx[j][g].y), f(acc[i][j][4 * g + 2] + bx[j][g].z), f(acc[i][j][4 * g + 3] + bx[j][g].w));
         } else {
-          T* base = reinterpret_cast<T*>(sec == 0 ? a.Q : a.Kt) + h * a.HD;
+          // 64-column groups [input 32 | gate 32] (blocks jp, jp + 1) -> output column (c / 64) * 32 + c % 64
 #pragma unroll
-          for (int it = 0; it < WTM / 8; it++) {
-            const int item = lane + 64 * it, r = item >> 3, q = item & 7;
-            const int row = rbase + r;
-            if (row < a.M)
-              *reinterpret_cast<u32x4_t*>(base + (size_t)row * a.ldqk + 8 * q) =
-                  *reinterpret_cast<const u32x4_t*>(wt + oidx(r, hb * 64 + 8 * q));
+          for (int jp = cp * CW / 16; jp < (cp + 1) * CW / 16; jp += 2)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+              const float4 x = bx[jp][g], y = bx[jp + 1][g];
+              const f32x16_t& p = acc[i][jp];
+              const f32x16_t& q = acc[i][jp + 1];
+              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(p[4 * g + 0] + x.x) * (q[4 * g + 0] + y.x),
+                   gelu_erf_as(p[4 * g + 1] + x.y) * (q[4 * g + 1] + y.y), gelu_erf_as(p[4 * g + 2] + x.z) * (q[4 * g + 2] + y.z),
+                   gelu_erf_as(p[4 * g + 3] + x.w) * (q[4 * g + 3] + y.w));
+            }
+        }
+        const int c0 = ocol + cp * CW;
+        flush(CPR, [&](int r) -> char* {
+          const int m = rbase + i * 32 + r;
+          return m < a.M ? reinterpret_cast<char*>(reinterpret_cast<T*>(a.C) + (size_t)m * a.ldc + c0) : nullptr;
+        }, nchunks(ncol - c0, 8, CPR));
+      }
+  } else {  // EPI_QKV: columns [q | k | v], each D = H * HD wide (HD == 64); q and k get RoPE
+    if (swap) {
+      constexpr int CW = fitw(WTN, SB / 64), CPR = CW / 8;
+      static_assert(CW % 64 == 0, "whole heads per staged block");
+      const bool rope = a.rope_cos != nullptr;
+      float* tcos = reinterpret_cast<float*>(&S0);
+      float* tsin = reinterpret_cast<float*>(&S1);
+      if (rope) {
+        // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each):
+        // position loads first, then the table loads, four 16-byte pieces per thread at a time
+        constexpr int NT = BM * 8 / 256;
+        int pp[NT];
+#pragma unroll
+        for (int k = 0; k < NT; k++) pp[k] = a.pos[min(m0 + ((tid + 256 * k) >> 3), a.M - 1)];
+#pragma unroll
+        for (int k0 = 0; k0 < NT; k0 += 4) {
+          float4 tc[4], ts[4];
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const int q = (tid + 256 * (k0 + k)) & 7;
+            tc[k] = *reinterpret_cast<const float4*>(a.rope_cos + pp[k0 + k] * 32 + 4 * q);
+            ts[k] = *reinterpret_cast<const float4*>(a.rope_sin + pp[k0 + k] * 32 + 4 * q);
           }
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const int it = tid + 256 * (k0 + k), r = it >> 3, q = it & 7;
+            *reinterpret_cast<float4*>(tcos + r * 32 + 4 * q) = tc[k];
+            *reinterpret_cast<float4*>(tsin + r * 32 + 4 * q) = ts[k];
+          }
+        }
+      }
+      float4 bx[FN][4];
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+      if (rope) __syncthreads();                          // tables complete
+      T* dst = reinterpret_cast<T*>(cbase < D ? a.Q : a.Kt) + (cbase % D);
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int r = wm * WTM + i * 32 + l32;            // row within the tile
+#pragma unroll
+        for (int cp = 0; cp < WTN / CW; cp++) {
+#pragma unroll
+          for (int jp = cp * CW / 32; jp < (cp + 1) * CW / 32; jp += 2)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+              const int dd = 8 * g + 4 * hi;
+              const float4 x0 = bx[jp][g], x1 = bx[jp + 1][g];
+              const float p1[4] = {acc[i][jp][4 * g + 0] + x0.x, acc[i][jp][4 * g + 1] + x0.y, acc[i][jp][4 * g + 2] + x0.z,
+                                   acc[i][jp][4 * g + 3] + x0.w};
+              const float p2[4] = {acc[i][jp + 1][4 * g + 0] + x1.x, acc[i][jp + 1][4 * g + 1] + x1.y,
+                                   acc[i][jp + 1][4 * g + 2] + x1.z, acc[i][jp + 1][4 * g + 3] + x1.w};
+              float o1[4], o2[4];
+              if (rope) {
+                // rotate_half partners (d, d + 32) of a head are blocks jp, jp + 1 of one lane
+                const f32x4_t cs = *reinterpret_cast<const f32x4_t*>(tcos + r * 32 + dd);
+                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(tsin + r * 32 + dd);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                  o1[u] = p1[u] * cs[u] - p2[u] * sn[u];
+                  o2[u] = p2[u] * cs[u] + p1[u] * sn[u];
+                }
+              } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++) { o1[u] = p1[u]; o2[u] = p2[u]; }
+              }
+              put8(l32, jp * 32 - cp * CW + dd, CPR, o1[0], o1[1], o1[2], o1[3]);
+              put8(l32, jp * 32 - cp * CW + 32 + dd, CPR, o2[0], o2[1], o2[2], o2[3]);
+            }
+          flush(CPR, [&](int rr) -> char* {
+            const int m = rbase + i * 32 + rr;
+            return m < a.M ? reinterpret_cast<char*>(dst + (size_t)m * a.ldqk + cp * CW) : nullptr;
+          }, CPR);
         }
       }
     } else {
-      const int ocol0 = EPI == EPI_GEGLU ? cbase / 2 : cbase;
-      const int ncols = EPI == EPI_GEGLU ? a.N / 2 : a.N;
+      // V^T[c - 2D][row]: lane holds four consecutive rows of one column per e / 4; staged as
+      // [column][row] blocks of 32 columns x CW rows, streamed out along rows of V^T (chunks that
+      // start past row M are not written)
+      constexpr int CW = fitw(WTM, SB / 64), CPR = CW / 8;
 #pragma unroll
-      for (int it = 0; it < WTM * CPRW / 64; it++) {
-        const int item = lane + 64 * it, r = item / CPRW, q = item % CPRW;
-        const int row = rbase + r, col = ocol0 + 8 * q;
-        if (row < a.M && col < ncols)
-          *reinterpret_cast<u32x4_t*>(reinterpret_cast<T*>(a.C) + (size_t)row * a.ldc + col) =
-              *reinterpret_cast<const u32x4_t*>(wt + oidx(r, 8 * q));
+      for (int j = 0; j < FN; j++) {
+        const int n = cbase + j * 32 + l32;
+        const float bv = (a.bias && n < a.N) ? a.bias[n] : 0.f;
+#pragma unroll
+        for (int cp = 0; cp < WTM / CW; cp++) {
+#pragma unroll
+          for (int i = cp * CW / 32; i < (cp + 1) * CW / 32; i++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, acc[i][j][4 * g + 0] + bv, acc[i][j][4 * g + 1] + bv,
+                   acc[i][j][4 * g + 2] + bv, acc[i][j][4 * g + 3] + bv);
+          const int r0 = rbase + cp * CW;
+          flush(CPR, [&](int rr) -> char* {
+            const int nn = cbase + j * 32 + rr;
+            return nn < a.N ? reinterpret_cast<char*>(reinterpret_cast<T*>(a.Vt) + (size_t)(nn - 2 * D) * a.ldv + r0) : nullptr;
+          }, nchunks(a.M - r0, 8, CPR));
+        }
       }
     }
   }
@@ -716,26 +804,31 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
   }
   switch (epi) {
     case EPI_RESID: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_RESID, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
-    case EPI_QKV: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_QKV, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_QKV:
+      if constexpr (BM <= BN) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_QKV, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a);
+      else { fprintf(stderr, "[laya] gemm: QKV tiles need BM <= BN\n"); exit(1); }
+      break;
     case EPI_GEGLU: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_GEGLU, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
     default: fprintf(stderr, "[laya] gemm: bad epilogue %d\n", epi); exit(1);
   }
 }
 
 // Tile configurations for the bf16 path and the planner that picks one per GEMM: estimated time
-// = rounds of concurrently resident tiles x per-tile cost, with the per-CU throughput of each
-// shape relative to 256x256.  Measured on MI355X at the ModernBERT-large shapes: two resident
-// 128x128 workgroups per CU (64 KiB of LDS each) beat one 256x256 workgroup by ~1.4x, because
-// one workgroup's epilogue (LDS staging, GELU/RoPE math, output stores) overlaps the other's
-// MFMA main loop, while a lone 256x256 workgroup leaves the MFMA pipe idle during its epilogue.
+// = rounds of concurrently resident tiles x per-tile cost, with each shape's throughput per tile
+// area relative to 256x256 (measured on MI355X at the ModernBERT-large shapes: one 256x256
+// workgroup per CU moves half the bytes per flop of a 128x128 pair and runs its K loop at ~78% of
+// the MFMA issue rate; two 128x128 workgroups per CU reach 0.73 of its rate, 256x128 and 128x256
+// 0.81).  Small M or N favour the smaller tiles through the rounds term.  QKV tiles must lie
+// inside one of the q/k/v sections (D % BN == 0) and need BM <= BN.
 struct XlCfg { int bm, bn, per_cu; float rel; };
-static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.90f}, {128, 256, 1, 0.90f}, {128, 128, 2, 1.40f}};
+static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.81f}, {128, 256, 1, 0.81f}, {128, 128, 2, 0.73f}};
 
-int gemm_pick(int M, int N, int /*epi*/) {
+static int gemm_pick(int M, int N, int epi, int D) {
   int best = -1;
   double bt = 1e300;
   for (int i = 0; i < (int)(sizeof(kXl) / sizeof(kXl[0])); i++) {
     const XlCfg& c = kXl[i];
+    if (epi == EPI_QKV && (c.bm > c.bn || D % c.bn)) continue;
     const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const double slots = 256.0 * c.per_cu;
     const double t = std::ceil(tiles / slots) * (double)c.bm * c.bn * c.per_cu / c.rel;
@@ -772,9 +865,15 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
                          (epi == EPI_RESID ? a.ldx % 4 == 0 : true) && (epi == EPI_QKV ? a.ldqk % 8 == 0 && a.ldv % 8 == 0 : true);
     const bool xl_ok = aligned && abytes < (1u << 31) - 65536 && wbytes < (1u << 31) - 65536;
     if (xl_ok) {
-      // LAYA_GEMM_CFG=0..3 pins one tile configuration (256x256, 256x128, 128x256, 128x128)
+      // LAYA_GEMM_CFG=0..3 pins one tile configuration (256x256, 256x128, 128x256, 128x128); QKV
+      // tiles must not straddle the q/k/v sections and need BM <= BN (RoPE tables in one stage)
       static const int forced = getenv("LAYA_GEMM_CFG") ? atoi(getenv("LAYA_GEMM_CFG")) : -1;
-      switch (forced >= 0 && forced < 4 ? forced : gemm_pick(a.M, a.N, epi)) {
+      const int D = a.H * a.HD;
+      int cfg = forced >= 0 && forced < 4 ? forced : gemm_pick(a.M, a.N, epi, D);
+      if (epi == EPI_QKV && cfg >= 0 && (kXl[cfg].bm > kXl[cfg].bn || D % kXl[cfg].bn))
+        cfg = gemm_pick(a.M, a.N, epi, D);               // a pinned shape QKV cannot use
+      switch (cfg) {
+        case -1: break;
         case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;
         case 1: launch_xl<256, 128, 2, 2>(epi, a, st); return;
         case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
