@@ -33,6 +33,21 @@ sys.path.insert(0, REPO)
 PEAK_BF16 = 2.5e15
 PEAK_FP32 = 157.3e12
 PEAK_HBM = 8.0e12
+PMC_COPY_BYTES = 256 << 20
+# calibrated HBM traffic per launch of the dominant kernel, from the committed rocprofv3 --pmc
+# summary (FETCH_SIZE and WRITE_SIZE runs of `bench.py --pmc-probe`, scaled by the copy kernel)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "c3_geglu_gemm_hbm_traffic.md")
+
+
+def measured_traffic(kernel_stage):
+    """Bytes per launch recorded for kernel_stage in the traffic summary, or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch ") and line.split()[1] == kernel_stage:
+                return int(line.split()[2])
+    except OSError:
+        pass
+    return None
 
 
 def stage_work(name, cfg, T, R, KT, B, elt, attn_flops):
@@ -97,6 +112,9 @@ def main():
     ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "c1"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: one plain copy of 256 MiB (the counter calibration), then "
+                         "three forward passes without graphs, then exit")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the decision pass is data parallel with no cross-GPU exchange, "
@@ -116,9 +134,22 @@ def main():
     mdir = ck.cached_checkpoint(cfg.name)
     print("[bench] checkpoint %s ready in %.1fs" % (mdir, time.time() - t0), file=sys.stderr, flush=True)
     max_tokens = max(16384, int(batch.tokens) + 1024)
-    eng = le.Engine(None, mdir, precision=precision, env={"LAYA_MAX_TOKENS": max_tokens, "LAYA_GRAPHS": 1,
+    eng = le.Engine(None, mdir, precision=precision, env={"LAYA_MAX_TOKENS": max_tokens,
+                                                         "LAYA_GRAPHS": 0 if a.pmc_probe else 1,
                                                          "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None})
     flat = batch.flat()
+    if a.pmc_probe:
+        src = torch.ones(PMC_COPY_BYTES, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)                                    # reads and writes exactly PMC_COPY_BYTES
+        torch.cuda.synchronize()
+        del src, dst
+        for _ in range(3):
+            eng.forward_flat(*flat)
+        torch.cuda.synchronize()
+        print("[bench] pmc probe done: copy of %d bytes, 3 passes of %s" % (PMC_COPY_BYTES, batch.name), file=sys.stderr)
+        return
     for _ in range(max(1, a.warmup)):
         eng.forward_flat(*flat)
     torch.cuda.synchronize()
@@ -185,12 +216,12 @@ def main():
         ach = fl / (dom_ms * 1e-3) / 1e12
         peak = (PEAK_BF16 if elt == 2 else PEAK_FP32) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4), "traffic": None, "kernel": dom,
+                "frac": round(ach / peak, 4), "traffic": measured_traffic(dom), "kernel": dom,
                 "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T)}
     else:
         ach = by / (dom_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": None, "kernel": dom}
+                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "kernel": dom}
 
     cpu = None
     if not a.no_cpu_baseline:
