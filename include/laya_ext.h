@@ -34,6 +34,13 @@ const char* laya_ext_precision(void* h);
 int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
                   int K, void* stream, int iters, float* ms);
 
+/* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 lets the planner
+ * choose per GEMM (the default, or LAYA_GEMM_CFG); 0..4 select 256x256, 256x128, 128x256, 128x128
+ * or 192x256 tiles (the QKV projection falls back to a shape that keeps its tiles inside one of
+ * the q/k/v sections).  Passes already captured in HIP graphs keep their kernels.  Returns the
+ * previous setting, or -2 for an invalid value. */
+int laya_ext_gemm_config(int cfg);
+
 #ifdef __cplusplus
 }
 #endif

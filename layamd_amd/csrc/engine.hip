@@ -611,4 +611,8 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
   return 0;
 }
 const char* laya_ext_precision(void* h) { return E(h)->precision(); }
+int laya_ext_gemm_config(int cfg) {
+  if (cfg < -1 || cfg > 4) return -2;
+  return laya::gemm_config(cfg);
+}
 }

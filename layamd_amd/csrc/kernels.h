@@ -42,6 +42,9 @@ struct GemmArgs {
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
+// pins the bf16 tile configuration for later launches (-1: the planner; 0..4: 256x256, 256x128,
+// 128x256, 128x128, 192x256); returns the previous setting
+int gemm_config(int cfg);
 
 // ---- attention over packed sequences ----
 // Query tiles from `tiles`; gathered mode when gq != null (queries are gathered rows

@@ -24,6 +24,8 @@
 
 #include "kernels.h"
 
+#include <atomic>
+
 namespace laya {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -611,7 +613,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   };
   auto nchunks = [](int valid_elems, int per_chunk, int cpr) { return max(0, min(cpr, (valid_elems + per_chunk - 1) / per_chunk)); };
   // widest power-of-two column count <= cap that divides w
-  constexpr auto fitw = [](int w, int cap) { int c = w; while (c > cap) c /= 2; return c; };
+  constexpr auto fitw = [](int w, int cap) { int c = w & -w; while (c > cap) c /= 2; return c; };
 
   if constexpr (EPI == EPI_RESID) {
     // fp32: blocks of 32 rows x CW columns
@@ -821,7 +823,29 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
 // 0.81).  Small M or N favour the smaller tiles through the rounds term.  QKV tiles must lie
 // inside one of the q/k/v sections (D % BN == 0) and need BM <= BN.
 struct XlCfg { int bm, bn, per_cu; float rel; };
-static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.81f}, {128, 256, 1, 0.81f}, {128, 128, 2, 0.73f}};
+static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.81f}, {128, 256, 1, 0.81f}, {128, 128, 2, 0.73f},
+                            {192, 256, 1, 0.95f}};
+
+// tile configuration pinned for every bf16 launch (-1: the planner); LAYA_GEMM_CFG sets it at the
+// first launch, gemm_config() at run time
+static std::atomic<int> g_gemm_cfg{-2};
+
+static int gemm_pinned() {
+  int v = g_gemm_cfg.load(std::memory_order_relaxed);
+  if (v == -2) {
+    const char* e = getenv("LAYA_GEMM_CFG");
+    v = e ? atoi(e) : -1;
+    if (v < -1 || v >= (int)(sizeof(kXl) / sizeof(kXl[0]))) v = -1;
+    g_gemm_cfg.store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+int gemm_config(int cfg) {
+  const int prev = gemm_pinned();
+  g_gemm_cfg.store(cfg, std::memory_order_relaxed);
+  return prev;
+}
 
 static int gemm_pick(int M, int N, int epi, int D) {
   int best = -1;
@@ -865,11 +889,12 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
                          (epi == EPI_RESID ? a.ldx % 4 == 0 : true) && (epi == EPI_QKV ? a.ldqk % 8 == 0 && a.ldv % 8 == 0 : true);
     const bool xl_ok = aligned && abytes < (1u << 31) - 65536 && wbytes < (1u << 31) - 65536;
     if (xl_ok) {
-      // LAYA_GEMM_CFG=0..3 pins one tile configuration (256x256, 256x128, 128x256, 128x128); QKV
-      // tiles must not straddle the q/k/v sections and need BM <= BN (RoPE tables in one stage)
-      static const int forced = getenv("LAYA_GEMM_CFG") ? atoi(getenv("LAYA_GEMM_CFG")) : -1;
+      // LAYA_GEMM_CFG=0..4 pins one tile configuration (256x256, 256x128, 128x256, 128x128,
+      // 192x256); QKV tiles must not straddle the q/k/v sections and need BM <= BN (RoPE tables in
+      // one stage)
+      const int forced = gemm_pinned();
       const int D = a.H * a.HD;
-      int cfg = forced >= 0 && forced < 4 ? forced : gemm_pick(a.M, a.N, epi, D);
+      int cfg = forced >= 0 ? forced : gemm_pick(a.M, a.N, epi, D);
       if (epi == EPI_QKV && cfg >= 0 && (kXl[cfg].bm > kXl[cfg].bn || D % kXl[cfg].bn))
         cfg = gemm_pick(a.M, a.N, epi, D);               // a pinned shape QKV cannot use
       switch (cfg) {
@@ -877,6 +902,7 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
         case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;
         case 1: launch_xl<256, 128, 2, 2>(epi, a, st); return;
         case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
+        case 4: launch_xl<192, 256, 2, 2>(epi, a, st); return;
         default: launch_xl<128, 128, 2, 2>(epi, a, st); return;
       }
     }

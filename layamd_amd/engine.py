@@ -24,7 +24,8 @@ HOST_LIB = os.path.join(PKG, "liblaya_host.so")
 
 ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act", "laya_max_len",
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
-EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm"]
+EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
+               "laya_ext_gemm_config"]
 
 _IP = ctypes.POINTER(ctypes.c_int)
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -70,6 +71,8 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
                                 ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 ctypes.c_void_p, ctypes.c_int, _FP]
     L.laya_ext_gemm.restype = ctypes.c_int
+    L.laya_ext_gemm_config.argtypes = [ctypes.c_int]
+    L.laya_ext_gemm_config.restype = ctypes.c_int
     return L
 
 
@@ -85,6 +88,14 @@ def gemm(lib, A, W, C, bias=None, act=0, residual=False, stream=None, iters=1):
     if rc != 0:
         raise ValueError("gemm shape rejected: M=%d N=%d K=%d" % (A.shape[0], W.shape[0], A.shape[1]))
     return ms.value
+
+
+def gemm_config(lib, cfg: int) -> int:
+    """Pins the bf16 GEMM tile configuration (-1: planner, 0..4: see laya_ext.h); returns the previous."""
+    prev = lib.laya_ext_gemm_config(cfg)
+    if prev == -2:
+        raise ValueError("invalid GEMM configuration %d" % cfg)
+    return prev
 
 
 def _ptr(a: np.ndarray, ct):

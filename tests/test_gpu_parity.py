@@ -64,12 +64,22 @@ def golden_flat_logits(c):
 
 
 # ---------------------------------------------------------------- GEMM kernel vs torch fp32
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+# bf16 runs every tile configuration of the MFMA GEMM (-1: the planner's choice)
+@pytest.mark.parametrize("dtype,cfg", [("fp32", -1)] + [("bf16", c) for c in (-1, 0, 1, 2, 3, 4)])
 @pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (200, 256, 320),
                                    (513, 1024, 2624)])
-def test_gemm_vs_torch(dtype, M, N, K):
+def test_gemm_vs_torch(dtype, cfg, M, N, K):
     import torch
     lib = le.load_library()
+    prev = le.gemm_config(lib, cfg)
+    try:
+        _check_gemm(lib, dtype, M, N, K)
+    finally:
+        le.gemm_config(lib, prev)
+
+
+def _check_gemm(lib, dtype, M, N, K):
+    import torch
     g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
     tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
     A = torch.randn(M, K, generator=g).to(tdt).cuda()
@@ -281,6 +291,24 @@ def test_large_bf16_c1_drift():
     upstream = prob_delta(g["logits_bf16_autocast"][0, :nm[0]], gl, nm)
     print("large bf16 dprob: engine %.5f, reference bf16 autocast %.5f" % (ours, upstream))
     assert ours < BF16_PROB
+
+
+def test_tile_configs_bit_identical():
+    """Every bf16 tile configuration runs the same K order through the same MFMA instruction, so the
+    whole pass (all 28 layers of ModernBERT-large, 32 questions of the b32 x s512 batch, split into
+    two passes) must give bit-identical outputs whichever tiles the GEMMs use."""
+    e = engine("large", "bf16", LAYA_GRAPHS=0)
+    b = wl.c3(0)
+    prev = le.gemm_config(e.lib, -1)
+    try:
+        ref_lo, ref_ac = e.forward_flat(*b.flat())
+        for cfg in (0, 1, 2, 3, 4):
+            le.gemm_config(e.lib, cfg)
+            lo, ac = e.forward_flat(*b.flat())
+            assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
+    finally:
+        le.gemm_config(e.lib, prev)
+    assert np.isfinite(ref_lo).all() and np.isfinite(ref_ac).all()
 
 
 def test_large_bf16_c3_sample_vs_oracle():
