@@ -28,6 +28,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-I" + CSRC, "-I" + INCLUDE,
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result"]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-I" + CSRC, "-I" + INCLUDE, "-Wall"]
+# attention keeps its small MFMA accumulators in VGPRs (the softmax works on them directly); the
+# GEMM keeps its large ones in AGPRs
+TU_FLAGS = {"kernels_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):
@@ -52,7 +55,7 @@ def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
     steps = []
     for s in HIP_SOURCES:
         src, obj = os.path.join(CSRC, s), os.path.join(BUILD, s + ".o")
-        steps.append((obj, [src] + headers, [HIPCC] + HIP_FLAGS + ["-c", src, "-o", obj]))
+        steps.append((obj, [src] + headers, [HIPCC] + HIP_FLAGS + TU_FLAGS.get(s, []) + ["-c", src, "-o", obj]))
     for s in CPP_SOURCES:
         src, obj = os.path.join(CSRC, s), os.path.join(BUILD, s + ".o")
         steps.append((obj, [src] + headers, ["g++"] + CXX_FLAGS + ["-c", src, "-o", obj]))

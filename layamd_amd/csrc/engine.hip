@@ -379,7 +379,7 @@ struct Engine : EngineIface {
         STAGE("enc:gemm_qkv_rope", launch_gemm<T>(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
-            launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, nullptr,
+            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, nullptr,
                                 nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
@@ -421,7 +421,7 @@ struct Engine : EngineIface {
         STAGE("head:gemm_qkv", launch_gemm<T>(EPI_QKV, g, st));
       }
       if (!last) {
-        STAGE("head:attn", launch_attention<T>(q, k, D, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen,
+        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen,
                                                nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
@@ -434,7 +434,7 @@ struct Engine : EngineIface {
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
-        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
+        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
                                                         d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
         { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D;

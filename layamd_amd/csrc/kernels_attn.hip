@@ -213,18 +213,256 @@ __global__ __launch_bounds__(256) void k_attention(const T* __restrict__ Q, cons
   }
 }
 
-template <typename T>
-void launch_attention(const T* Q, const T* K, int ldqk, const T* Vt, int ldv, T* O, int ldo, const AttnTile* tiles,
-                      int ntiles, int H, const int* soff, const int* vlen, const int* gq, const int* grow,
-                      int window_half, float scale, hipStream_t st) {
-  if (ntiles <= 0) return;
-  hipLaunchKernelGGL((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
-                     vlen, gq, grow, window_half, scale);
+__device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-template void launch_attention<float>(const float*, const float*, int, const float*, int, float*, int, const AttnTile*,
-                                      int, int, const int*, const int*, const int*, const int*, int, float, hipStream_t);
-template void launch_attention<bf16_t>(const bf16_t*, const bf16_t*, int, const bf16_t*, int, bf16_t*, int,
+// ======================================================================================
+// bf16 attention (v_mfma_f32_32x32x16_bf16).  One 128-thread workgroup owns one query tile (<= 64
+// queries of one sequence) of one head; each of its two waves owns 32 queries, so every K and V^T
+// fragment read from LDS feeds a 32-query MFMA.  Keys advance in blocks of 64, double-buffered in
+// LDS: the block after the current one is fetched by LDS DMA (inline assembly, as in the GEMM)
+// while the current one is multiplied, with one wait and one barrier per block.
+//
+//   S^T[key][query] = K Q^T   A = K rows (32 keys x 16 d per MFMA), B = Q rows (registers)
+//   O^T[d][query] += V^T P^T  A = V^T rows (32 d x 16 keys),       B = P^T from the S^T registers
+//
+// The 32x32 accumulator gives lane l query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of a
+// 32-key sub-block, so lanes l and l ^ 32 together hold a query's 64 scores: row max and row sum
+// take one cross-lane step.  Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand
+// of one 16-key PV step with k-index i <-> key 16 h' + 8 (i / 4) + 4 (l / 32) + i % 4; the V^T
+// operand reads the same keys (two 8-byte pieces per lane).  Scores are scaled into the log2
+// domain once (exp2); blocks whose keys are all visible to every query of the tile skip the mask.
+// ======================================================================================
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// LDS DMA of one 16-byte chunk per lane (see the GEMM's dma16: M0 is the LDS base, the whole
+// offset is range-checked, the memory clobber orders it against LDS reads)
+__device__ __forceinline__ void attn_dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
+__device__ __forceinline__ u32x4_t attn_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  u32x4_t r;
+  r[0] = (uint32_t)v;
+  r[1] = (uint32_t)(v >> 32) & 0xFFFFu;
+  r[2] = bytes;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+__global__ __launch_bounds__(128) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
+                                                        int ldqk, int kv_rows, const bf16_t* __restrict__ Vt, int ldv,
+                                                        int vt_rows, bf16_t* __restrict__ O, int ldo,
+                                                        const AttnTile* __restrict__ tiles, const int* __restrict__ soff,
+                                                        const int* __restrict__ vlen, const int* __restrict__ gq,
+                                                        const int* __restrict__ grow, int window_half, float scale) {
+  constexpr int HD = 64;
+  // [buffer][row][8 chunks of 16 bytes]: K rows are keys, V^T rows are d; chunk c of row r sits at
+  // position c ^ ((r >> 1) & 7), so 16 lanes reading one chunk of 16 consecutive rows hit 16
+  // distinct 16-byte bank positions
+  __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs0[64 * 8], Vs1[64 * 8];
+
+  // heads are the fastest grid dimension, so the (longest-first) tiles start in order
+  const AttnTile tile = tiles[blockIdx.y];
+  const int h = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+  const int b = tile.seq, len = vlen[b], base = soff[b];
+
+  // this lane's query (32 per wave)
+  const int r = wave * 32 + l32;
+  const bool qvalid = r < tile.nq;
+  const int rr = qvalid ? r : 0;
+  int p, orow;
+  if (gq) { const int gi = gq[tile.q0 + rr]; p = grow[gi] - base; orow = gi; }
+  else { p = tile.q0 + rr; orow = base + p; }
+
+  // key range of the tile and the range whose blocks need no mask
+  int lo = 0, hi_k = len;
+  int full_lo = 0, full_hi = len;                         // keys visible to every query of the tile
+  if (window_half > 0 && !gq) {
+    const int pmin = tile.q0, pmax = tile.q0 + tile.nq - 1;
+    lo = max(0, pmin - window_half) & ~15;
+    hi_k = min(len, pmax + window_half + 1);
+    full_lo = pmax - window_half;
+    full_hi = min(len, pmin + window_half + 1);
+  }
+
+  // keys visible to this lane's query: [jlo, jhi)
+  const int jlo = (window_half > 0 && !gq) ? max(0, p - window_half) : 0;
+  const int jhi = (window_half > 0 && !gq) ? min(len, p + window_half + 1) : len;
+
+  // Q fragments (B operand): query row, d = 16 s + 8 hi .. + 7
+  const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(Q + (size_t)(base + p) * ldqk + h * HD);
+  u32x4_t qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) qf[s] = qrow[2 * s + hi];
+
+  // DMA plan: instruction j (0..3 per wave) fills rows 8 (4 wave + j) .. + 7 of the K block and of
+  // the V^T block; lane -> row + lane / 8, position lane % 8 (global chunk position ^ swizzle)
+  const u32x4_t rK = attn_rsrc(K, (uint32_t)((size_t)kv_rows * ldqk * 2));
+  const u32x4_t rV = attn_rsrc(Vt, (uint32_t)((size_t)vt_rows * ldv * 2));
+  uint32_t kvo[4], vvo[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int row = 8 * (4 * wave + j) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+    kvo[j] = ((uint32_t)(base + row) * (uint32_t)ldqk + (uint32_t)(h * HD)) * 2u + (uint32_t)c * 16u;
+    vvo[j] = ((uint32_t)(h * HD + row) * (uint32_t)ldv + (uint32_t)base) * 2u + (uint32_t)c * 16u;
+  }
+  const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 4u * 1024u;
+  auto fetch = [&](int k0, u32x4_t* ks, u32x4_t* vs) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
+      attn_dma16(rV, lds_addr_a(vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
+    }
+  };
+
+  f32x16_t o[2];
+#pragma unroll
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[db][e] = 0.f;
+  // running max of the raw scores (scale > 0 keeps the order) and running sum; probabilities are
+  // exp2(s * c - m * c) with c = scale * log2(e), one FMA per score
+  float m_run = -INFINITY, l_run = 0.f;
+  const float c2 = scale * 1.44269504088896340736f;
+
+  fetch(lo, Ks0, Vs0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  const int sw = (l32 >> 1) & 7;                           // swizzle of fragment rows 32 n + l32
+  int it = 0;
+  for (int k0 = lo; k0 < hi_k; k0 += 64, ++it) {
+    const bool odd = it & 1;
+    const u32x4_t* ks = odd ? Ks1 : Ks0;
+    const u32x4_t* vs = odd ? Vs1 : Vs0;
+    if (k0 + 64 < hi_k) {
+      if (odd) fetch(k0 + 64, Ks0, Vs0);
+      else fetch(k0 + 64, Ks1, Vs1);
+    }
+
+    // ---- S^T = K Q^T: two 32-key sub-blocks ----
+    f32x16_t st[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) st[kb][e] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const u32x4_t kf = ks[(32 * kb + l32) * 8 + ((2 * s + hi) ^ sw)];
+        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                         __builtin_bit_cast(bf16x8_t, qf[s]), st[kb], 0, 0, 0);
+      }
+    }
+
+    // ---- mask, online softmax (branch-free per lane) ----
+    const bool full = k0 >= full_lo && k0 + 64 <= full_hi;
+    float mx = -INFINITY;
+    if (full) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, st[kb][e]);
+    } else {
+      // visible keys of this lane's query: [jlo, jhi)
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int j = k0 + 32 * kb + 8 * (e >> 2) + 4 * hi + (e & 3);
+          st[kb][e] = (unsigned)(j - jlo) < (unsigned)(jhi - jlo) ? st[kb][e] : -INFINITY;
+          mx = fmaxf(mx, st[kb][e]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    // with no visible key yet (m_new = -inf) every exp2 below is exp2(-inf) = 0
+    const float mc = m_new == -INFINITY ? 0.f : m_new * c2;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        st[kb][e] = __builtin_amdgcn_exp2f(fmaf(st[kb][e], c2, -mc));
+        rs += st[kb][e];
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    // the running output is rescaled only when some lane's max moved (alpha == 1 otherwise)
+    if (__any(m_new != m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, -mc));
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; db++) o[db] *= alpha;
+    }
+    l_run += rs;
+    m_run = m_new;
+
+    // ---- O^T += V^T P^T: four 16-key steps ----
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const f32x16_t& sp = st[kk >> 1];
+      const int e0 = 8 * (kk & 1);
+      bf16x8_t pb;
+#pragma unroll
+      for (int i = 0; i < 8; i++) pb[i] = (__bf16)sp[e0 + i];
+#pragma unroll
+      for (int db = 0; db < 2; db++) {
+        const int d = 32 * db + l32;
+        const u32x2_t* vrow = reinterpret_cast<const u32x2_t*>(vs + d * 8);
+        // keys 16 kk + 4 hi + (0..3): chunk 2 kk, half hi; keys 16 kk + 8 + 4 hi + (0..3): chunk 2 kk + 1
+        const u32x2_t u0 = vrow[2 * ((2 * kk) ^ ((d >> 1) & 7)) + hi];
+        const u32x2_t u1 = vrow[2 * ((2 * kk + 1) ^ ((d >> 1) & 7)) + hi];
+        const u32x4_t va = (u32x4_t){u0.x, u0.y, u1.x, u1.y};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pb, o[db], 0, 0, 0);
+      }
+    }
+    // the next block has landed (this wave's part) and no wave still reads the current buffers
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+
+  if (!qvalid) return;
+  // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  bf16_t* orow_p = O + (size_t)orow * ldo + h * HD;
+#pragma unroll
+  for (int db = 0; db < 2; db++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = 32 * db + 8 * g + 4 * hi;
+      u32x2_t u;
+      u[0] = (uint32_t)f2bf(o[db][4 * g + 0] * inv) | ((uint32_t)f2bf(o[db][4 * g + 1] * inv) << 16);
+      u[1] = (uint32_t)f2bf(o[db][4 * g + 2] * inv) | ((uint32_t)f2bf(o[db][4 * g + 3] * inv) << 16);
+      *reinterpret_cast<u32x2_t*>(orow_p + d) = u;
+    }
+}
+
+template <typename T>
+void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt, int ldv, T* O, int ldo,
+                      const AttnTile* tiles, int ntiles, int H, const int* soff, const int* vlen, const int* gq,
+                      const int* grow, int window_half, float scale, hipStream_t st) {
+  if (ntiles <= 0) return;
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL(k_attention_bf16, dim3(H, ntiles), dim3(128), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O, ldo,
+                       tiles, soff, vlen, gq, grow, window_half, scale);
+  } else {
+    hipLaunchKernelGGL((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
+                       vlen, gq, grow, window_half, scale);
+  }
+}
+
+template void launch_attention<float>(const float*, const float*, int, int, const float*, int, float*, int,
+                                      const AttnTile*, int, int, const int*, const int*, const int*, const int*, int,
+                                      float, hipStream_t);
+template void launch_attention<bf16_t>(const bf16_t*, const bf16_t*, int, int, const bf16_t*, int, bf16_t*, int,
                                        const AttnTile*, int, int, const int*, const int*, const int*, const int*, int,
                                        float, hipStream_t);
 

@@ -68,6 +68,12 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
         p.gq.insert(p.gq.end(), q.begin() + s, q.begin() + s + cnt);
       }
     }
+    // longest questions first: an attention launch then starts its longest tiles (which visit the
+    // most key blocks) before the short ones instead of ending on them (tile order does not change
+    // any result)
+    auto by_len = [&](const AttnTile& x, const AttnTile& y) { return p.vlen[x.seq] > p.vlen[y.seq]; };
+    std::stable_sort(p.tiles.begin(), p.tiles.end(), by_len);
+    std::stable_sort(p.gtiles.begin(), p.gtiles.end(), by_len);
     passes->push_back(std::move(p));
     b0 += n;
   }
