@@ -25,6 +25,7 @@
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <thread>
 #include <tuple>
@@ -87,6 +88,7 @@ struct EngineIface {
                             const int* qtypes, float* logits, float* act) = 0;
   virtual int replay(int iters, float* ms) = 0;
   virtual void warmup() = 0;
+  virtual void tune_all() = 0;
   virtual const char* precision() const = 0;
 };
 
@@ -131,6 +133,14 @@ struct Engine : EngineIface {
   std::map<Shape, hipGraphExec_t> graphs;
   bool have_last = false;
   Shape last{};
+
+  // measured bf16 tile configuration per (epilogue, activation, N, K, RoPE, M bucket), filled before
+  // the first pass of a shape (or by tune_all); every configuration gives bit-identical results
+  using TuneKey = std::tuple<int, int, int, int, int, int>;
+  std::map<TuneKey, int> tuned;
+  std::set<Shape> tuned_shapes;
+  bool tune_on = true;
+  std::vector<std::pair<int, GemmArgs>>* collecting = nullptr;   // set while a pass's GEMMs are listed
 
   const char* precision() const override { return sizeof(T) == 2 ? "bf16" : "fp32"; }
 
@@ -315,6 +325,7 @@ struct Engine : EngineIface {
     LAYA_HIP(hipStreamCreate(&stream));
     prof.init();
     use_graphs = env_int("LAYA_GRAPHS", 1) != 0;
+    tune_on = env_int("LAYA_TUNE", 1) != 0;
     dump_dir = getenv("LAYA_DUMP_DIR");
     if (dump_dir && !*dump_dir) dump_dir = nullptr;
     LAYA_HIP(hipDeviceSynchronize());
@@ -335,7 +346,7 @@ struct Engine : EngineIface {
   }
 
   void dump(const char* name, const float* dev, size_t rows) {
-    if (!dump_dir || capturing) return;
+    if (!dump_dir || capturing || collecting) return;
     LAYA_HIP(hipStreamSynchronize(stream));
     std::vector<float> buf(rows * cfg.d);
     LAYA_HIP(hipMemcpy(buf.data(), dev, buf.size() * 4, hipMemcpyDeviceToHost));
@@ -350,6 +361,92 @@ struct Engine : EngineIface {
     return g;
   }
 
+  // ------------------------------------------------------------ GEMM tile tuning
+  // M buckets: multiples of 64 rows up to 1024, then 32 buckets per octave
+  static int m_bucket(int M) {
+    if (M <= 1024) return (M + 63) / 64 * 64;
+    const int step = 1 << (31 - __builtin_clz((unsigned)M) - 5);
+    return (M + step - 1) / step * step;
+  }
+  static TuneKey tune_key(int epi, const GemmArgs& g) {
+    return TuneKey(epi, g.act, g.N, g.K, g.rope_cos != nullptr, m_bucket(g.M));
+  }
+
+  // one GEMM of the pass: listed while the pass is collected for tuning, otherwise launched with
+  // the measured configuration of its bucket (the analytic planner's where none was measured)
+  void gemm(int epi, GemmArgs g, hipStream_t st) {
+    if (collecting) { collecting->emplace_back(epi, g); return; }
+    auto it = tuned.find(tune_key(epi, g));
+    if (it != tuned.end()) g.cfg = it->second;
+    launch_gemm<T>(epi, g, st);
+  }
+
+  // Times every tile configuration this GEMM can use, at its own M, on its own buffers (which hold
+  // nothing live before a pass), and returns the fastest: the analytic pick unless another one is
+  // more than 3% faster.  The operand rows are first filled with a finite pattern so the timing
+  // sees realistic MFMA power and the V^T rows a QKV candidate writes stay finite.
+  int tune_gemm(int epi, GemmArgs g) {
+    const int first = gemm_planned(epi, g);
+    if (first < 0) return -1;
+    launch_fill_pattern((T*)const_cast<void*>(g.A), (size_t)g.M * g.lda, 0x9E3779B9u ^ (uint32_t)g.K, stream);
+    hipEvent_t a, b;
+    LAYA_HIP(hipEventCreate(&a));
+    LAYA_HIP(hipEventCreate(&b));
+    const int reps = g.M >= 2048 ? 3 : 8;
+    int best = first;
+    float bt = 1e30f;
+    for (int i = -1; i < kGemmConfigs; i++) {
+      const int c = i < 0 ? first : i;
+      if ((i >= 0 && c == first) || !gemm_config_valid(epi, g, c)) continue;
+      g.cfg = c;
+      launch_gemm<T>(epi, g, stream);
+      LAYA_HIP(hipEventRecord(a, stream));
+      for (int r = 0; r < reps; r++) launch_gemm<T>(epi, g, stream);
+      LAYA_HIP(hipEventRecord(b, stream));
+      LAYA_HIP(hipEventSynchronize(b));
+      float ms = 0.f;
+      LAYA_HIP(hipEventElapsedTime(&ms, a, b));
+      ms /= reps;
+      if (verbose) printf("[laya] tune epi %d %5dx%5dx%5d cfg %d: %8.1f us\n", epi, g.M, g.N, g.K, c, ms * 1e3f);
+      if (ms < bt * 0.97f) { bt = ms; best = c; }
+    }
+    LAYA_HIP(hipEventDestroy(a));
+    LAYA_HIP(hipEventDestroy(b));
+    return best;
+  }
+
+  // lists the GEMMs of pass shape s (uploading its index arrays, which the QKV epilogue reads) and
+  // tunes the buckets not yet measured
+  void tune_pass(const Shape& s) {
+    if (!tune_on || sizeof(T) != 2 || gemm_pinned() >= 0 || capturing || tuned_shapes.count(s)) return;
+    std::vector<std::pair<int, GemmArgs>> list;
+    collecting = &list;
+    run(s);
+    collecting = nullptr;
+    for (auto& eg : list) {
+      const TuneKey key = tune_key(eg.first, eg.second);
+      if (!tuned.count(key)) tuned[key] = tune_gemm(eg.first, eg.second);
+    }
+    LAYA_HIP(hipStreamSynchronize(stream));
+    tuned_shapes.insert(s);
+  }
+
+  // every M bucket up to the pass capacity, for every GEMM of the model (the gathered head rows and
+  // the scorer share the encoder's and head's (N, K) shapes at other M)
+  void tune_all() override {
+    if (tune_on && sizeof(T) == 2 && gemm_pinned() < 0) {
+      // the listing run uploads these host mirrors: position 0 keeps the RoPE table reads in range
+      for (int64_t i = 0; i < MT; i++) { h_pos[i] = 0; h_seq[i] = 0; h_ids[i] = 0; }
+      for (int64_t i = 0; i < RG; i++) { h_gq[i] = 0; h_grow[i] = 0; }
+      h_soff[0] = 0; h_soff[1] = 0; h_vlen[0] = 0; h_qt[0] = 0; h_nm[0] = 0; h_moff[0] = 0;
+      for (int mb = 64; mb <= MT; mb = m_bucket(mb + 1)) {
+        const int r = (int)std::min<int64_t>(mb, RG);
+        tune_pass(Shape{mb, 1, r - 1, r, 0, 0});
+      }
+    }
+    warmup();
+  }
+
   void run(const Shape& s) {
     const int D = cfg.d, H = cfg.n_heads, HD = cfg.head_dim, I = cfg.intermediate, FF = cfg.head_ffn;
     const float eps = cfg.norm_eps, scale = 1.0f / sqrtf((float)HD);
@@ -362,7 +459,9 @@ struct Engine : EngineIface {
     h2d(d_gq, h_gq, R * 4); h2d(d_grow, h_grow, R * 4);
     h2d(d_tiles, h_tiles, s.nt * sizeof(AttnTile)); h2d(d_gtiles, h_gtiles, s.ngt * sizeof(AttnTile));
 
-#define STAGE(name, ...) do { prof.start(st); __VA_ARGS__; prof.stop(name, st); } while (0)
+    // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
+#define STAGE(name, ...) do { if (!collecting) { prof.start(st); __VA_ARGS__; prof.stop(name, st); } } while (0)
+#define GSTAGE(name, ...) do { if (collecting) { __VA_ARGS__; } else { prof.start(st); __VA_ARGS__; prof.stop(name, st); } } while (0)
     STAGE("enc:embed_ln", launch_layernorm<T, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
                                                  nullptr, x, enc[0].attn_norm ? nullptr : xn, st));
     dump("emb", x, T_);
@@ -376,7 +475,7 @@ struct Engine : EngineIface {
         GemmArgs g = gemm_args(xn, D, e.Wqkv, T_, 3 * D, D, nullptr);
         g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
         g.rope_cos = glob ? cos_g : cos_l; g.rope_sin = glob ? sin_g : sin_l;
-        STAGE("enc:gemm_qkv_rope", launch_gemm<T>(EPI_QKV, g, st));
+        GSTAGE("enc:gemm_qkv_rope", gemm(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
             launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, nullptr,
@@ -384,19 +483,19 @@ struct Engine : EngineIface {
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
         g.X = x; g.ldx = D;
-        STAGE("enc:gemm_attn_out_res", launch_gemm<T>(EPI_RESID, g, st));
+        GSTAGE("enc:gemm_attn_out_res", gemm(EPI_RESID, g, st));
       }
       STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.mlp_norm, nullptr, nullptr, nullptr, nullptr,
                                                  nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, e.Wi, T_, 2 * I, D, nullptr);
         g.C = mg; g.ldc = I;
-        STAGE("enc:gemm_mlp_in_geglu", launch_gemm<T>(EPI_GEGLU, g, st));
+        GSTAGE("enc:gemm_mlp_in_geglu", gemm(EPI_GEGLU, g, st));
       }
       {
         GemmArgs g = gemm_args(mg, I, e.Wmo, T_, D, I, nullptr);
         g.X = x; g.ldx = D;
-        STAGE("enc:gemm_mlp_out_res", launch_gemm<T>(EPI_RESID, g, st));
+        GSTAGE("enc:gemm_mlp_out_res", gemm(EPI_RESID, g, st));
       }
       if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "enc%d", L); dump(nm, x, T_); }
       if (L + 1 < cfg.n_layers) {
@@ -418,19 +517,19 @@ struct Engine : EngineIface {
       {
         GemmArgs g = gemm_args(xn, D, hl.inW, T_, 3 * D, D, hl.inB);
         g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
-        STAGE("head:gemm_qkv", launch_gemm<T>(EPI_QKV, g, st));
+        GSTAGE("head:gemm_qkv", gemm(EPI_QKV, g, st));
       }
       if (!last) {
         STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen,
                                                nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
-          STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
+          GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
         STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
                                                     nullptr, xn, st));
         { GemmArgs g = gemm_args(xn, D, hl.l1W, T_, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
-          STAGE("head:gemm_ffn1_relu", launch_gemm<T>(EPI_STORE, g, st)); }
+          GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
         { GemmArgs g = gemm_args(ff, FF, hl.l2W, T_, D, FF, hl.l2B); g.X = x; g.ldx = D;
-          STAGE("head:gemm_ffn2_res", launch_gemm<T>(EPI_RESID, g, st)); }
+          GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
@@ -438,13 +537,13 @@ struct Engine : EngineIface {
                                                         d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
         { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D;
-          STAGE("head:gemm_out_res", launch_gemm<T>(EPI_RESID, g, st)); }
+          GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
         STAGE("head:ln", launch_layernorm<float, T>(xg, nullptr, R, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
                                                     nullptr, xng, st));
         { GemmArgs g = gemm_args(xng, D, hl.l1W, R, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
-          STAGE("head:gemm_ffn1_relu", launch_gemm<T>(EPI_STORE, g, st)); }
+          GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
         { GemmArgs g = gemm_args(ff, FF, hl.l2W, R, D, FF, hl.l2B); g.X = xg; g.ldx = D;
-          STAGE("head:gemm_ffn2_res", launch_gemm<T>(EPI_RESID, g, st)); }
+          GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d_gathered", L); dump(nm, xg, R); }
       }
     }
@@ -452,11 +551,13 @@ struct Engine : EngineIface {
     STAGE("scorer:ln", launch_layernorm<float, T>(xg, nullptr, KT, D, eps, sc0w, sc0b, nullptr, nullptr, nullptr,
                                                   nullptr, xng, st));
     { GemmArgs g = gemm_args(xng, D, sc1W, KT, D, D, sc1b); g.C = sh; g.ldc = D; g.act = ACT_GELU;
-      STAGE("scorer:gemm_gelu", launch_gemm<T>(EPI_STORE, g, st)); }
+      GSTAGE("scorer:gemm_gelu", gemm(EPI_STORE, g, st)); }
     STAGE("scorer:dot", launch_row_dot<T>(sh, D, sc3w, sc3b, d_logits, KT, D, st));
     STAGE("act_head", launch_act_head(xg + (size_t)KT * D, D, d_logits, d_moff, d_nm, ah0W, ah0b, ah2W, ah2b,
                                       cfg.n_act, d_act, d_act_hidden, B, st));
 #undef STAGE
+#undef GSTAGE
+    if (collecting) return;
     LAYA_HIP(hipMemcpyAsync(h_logits, d_logits, (size_t)KT * 4, hipMemcpyDeviceToHost, st));
     LAYA_HIP(hipMemcpyAsync(h_act, d_act, (size_t)B * cfg.n_act * 4, hipMemcpyDeviceToHost, st));
   }
@@ -473,6 +574,7 @@ struct Engine : EngineIface {
         return;
       }
     }
+    tune_pass(s);
     run(s);
     LAYA_HIP(hipStreamSynchronize(stream));
     if (!graphs_on || graphs.size() >= 512) return;
@@ -573,7 +675,7 @@ float laya_temperature(void* h, int qtype) {
 }
 void laya_prof_report(void* h, int iters) { E(h)->prof.report(iters); }
 void laya_prof_reset(void* h) { E(h)->prof.acc.clear(); }
-void laya_tune_all(void* h) { E(h)->warmup(); }
+void laya_tune_all(void* h) { E(h)->tune_all(); }
 
 int laya_ext_prof_enable(void* h, int on) { int was = E(h)->prof.on; E(h)->prof.on = on != 0; return was; }
 int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, long long* calls) {

@@ -18,6 +18,9 @@ void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float ep
 
 // xg[r] = x[rows[r]] (fp32 rows of width D)
 void launch_gather_rows(const float* x, const int* rows, float* xg, int R, int D, hipStream_t st);
+// finite pattern in [-1, 1) over n elements (GEMM tuning operands)
+template <typename T>
+void launch_fill_pattern(T* p, size_t n, uint32_t seed, hipStream_t st);
 
 // ---- MFMA GEMM: C = A[M,K] . W[N,K]^T with a fused epilogue ----
 enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GEGLU = 3 };
@@ -37,6 +40,7 @@ struct GemmArgs {
   int H = 0, HD = 0;
   const int* pos = nullptr;                      // RoPE position of each row
   const float* rope_cos = nullptr; const float* rope_sin = nullptr;  // [positions][HD/2]
+  int cfg = -1;                                  // bf16 tile configuration (-1: the planner's pick)
 };
 
 template <typename T>
@@ -45,6 +49,12 @@ bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
 // pins the bf16 tile configuration for later launches (-1: the planner; 0..4: 256x256, 256x128,
 // 128x256, 128x128, 192x256); returns the previous setting
 int gemm_config(int cfg);
+int gemm_pinned();                               // the pinned configuration, or -1
+constexpr int kGemmConfigs = 5;
+// whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
+// shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)
+bool gemm_config_valid(int epi, const GemmArgs& a, int cfg);
+int gemm_planned(int epi, const GemmArgs& a);
 
 // ---- attention over packed sequences ----
 // Query tiles from `tiles`; gathered mode when gq != null (queries are gathered rows

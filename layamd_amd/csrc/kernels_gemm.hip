@@ -815,27 +815,28 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
   }
 }
 
-// Tile configurations for the bf16 path and the planner that picks one per GEMM: estimated time
-// = rounds of concurrently resident tiles x per-tile cost, with each shape's throughput per tile
-// area relative to 256x256 (measured on MI355X at the ModernBERT-large shapes: one 256x256
-// workgroup per CU moves half the bytes per flop of a 128x128 pair and runs its K loop at ~78% of
-// the MFMA issue rate; two 128x128 workgroups per CU reach 0.73 of its rate, 256x128 and 128x256
-// 0.81).  Small M or N favour the smaller tiles through the rounds term.  QKV tiles must lie
-// inside one of the q/k/v sections (D % BN == 0) and need BM <= BN.
+// Tile configurations for the bf16 path and the analytic planner that picks one per GEMM when no
+// measured choice is given: estimated time = rounds of concurrently resident tiles x per-tile
+// cost, with each shape's throughput per tile area relative to 256x256 (measured on MI355X at the
+// ModernBERT-large shapes; it varies with K and the epilogue, which is why the engine times the
+// candidates instead where it can).  One-workgroup-per-CU shapes run in lockstep rounds (a partial
+// last round costs a whole one); two 128x128 workgroups per CU interleave, so their partial rounds
+// cost their fraction.  QKV tiles must lie inside one of the q/k/v sections (D % BN == 0) and need
+// BM <= BN.
 struct XlCfg { int bm, bn, per_cu; float rel; };
-static const XlCfg kXl[] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.81f}, {128, 256, 1, 0.81f}, {128, 128, 2, 0.73f},
-                            {192, 256, 1, 0.95f}};
+static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80f}, {128, 256, 1, 0.83f},
+                                        {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}};
 
-// tile configuration pinned for every bf16 launch (-1: the planner); LAYA_GEMM_CFG sets it at the
-// first launch, gemm_config() at run time
+// tile configuration pinned for every bf16 launch (-1: none); LAYA_GEMM_CFG sets it at the first
+// launch, gemm_config() at run time
 static std::atomic<int> g_gemm_cfg{-2};
 
-static int gemm_pinned() {
+int gemm_pinned() {
   int v = g_gemm_cfg.load(std::memory_order_relaxed);
   if (v == -2) {
     const char* e = getenv("LAYA_GEMM_CFG");
     v = e ? atoi(e) : -1;
-    if (v < -1 || v >= (int)(sizeof(kXl) / sizeof(kXl[0]))) v = -1;
+    if (v < -1 || v >= kGemmConfigs) v = -1;
     g_gemm_cfg.store(v, std::memory_order_relaxed);
   }
   return v;
@@ -845,20 +846,6 @@ int gemm_config(int cfg) {
   const int prev = gemm_pinned();
   g_gemm_cfg.store(cfg, std::memory_order_relaxed);
   return prev;
-}
-
-static int gemm_pick(int M, int N, int epi, int D) {
-  int best = -1;
-  double bt = 1e300;
-  for (int i = 0; i < (int)(sizeof(kXl) / sizeof(kXl[0])); i++) {
-    const XlCfg& c = kXl[i];
-    if (epi == EPI_QKV && (c.bm > c.bn || D % c.bn)) continue;
-    const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const double slots = 256.0 * c.per_cu;
-    const double t = std::ceil(tiles / slots) * (double)c.bm * c.bn * c.per_cu / c.rel;
-    if (t < bt * 0.999) { bt = t; best = i; }
-  }
-  return best;
 }
 
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) {
@@ -875,6 +862,45 @@ bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) 
   return true;
 }
 
+// the tiled bf16 kernel needs 16-byte epilogue stores (N, the row strides and the output bases in
+// multiples of 8 elements) and operands that 32-bit buffer offsets reach
+static bool xl_usable(int epi, const GemmArgs& a) {
+  const size_t abytes = (size_t)a.M * a.lda * 2, wbytes = (size_t)a.N * a.ldw * 2;
+  const bool aligned = a.N % 8 == 0 && ((epi == EPI_STORE || epi == EPI_GEGLU) ? a.ldc % 8 == 0 : true) &&
+                       (epi == EPI_RESID ? a.ldx % 4 == 0 : true) && (epi == EPI_QKV ? a.ldqk % 8 == 0 && a.ldv % 8 == 0 : true);
+  return aligned && abytes < (1u << 31) - 65536 && wbytes < (1u << 31) - 65536;
+}
+
+static bool xl_cfg_fits(int epi, const GemmArgs& a, int cfg) {
+  if (cfg < 0 || cfg >= kGemmConfigs) return false;
+  return epi != EPI_QKV || (kXl[cfg].bm <= kXl[cfg].bn && (a.H * a.HD) % kXl[cfg].bn == 0);
+}
+
+static int gemm_pick(int epi, const GemmArgs& a) {
+  int best = -1;
+  double bt = 1e300;
+  for (int i = 0; i < kGemmConfigs; i++) {
+    if (!xl_cfg_fits(epi, a, i)) continue;
+    const XlCfg& c = kXl[i];
+    const double tiles = (double)((a.M + c.bm - 1) / c.bm) * ((a.N + c.bn - 1) / c.bn);
+    const double slots = 256.0 * c.per_cu;
+    const double rounds = c.per_cu > 1 ? std::max(1.0, tiles / slots) : std::ceil(tiles / slots);
+    const double t = rounds * (double)c.bm * c.bn * c.per_cu / c.rel;
+    if (t < bt * 0.999) { bt = t; best = i; }
+  }
+  return best;
+}
+
+bool gemm_config_valid(int epi, const GemmArgs& a, int cfg) {
+  const char* why = "";
+  return gemm_shape_ok(epi, a, 2, &why) && xl_usable(epi, a) && xl_cfg_fits(epi, a, cfg);
+}
+
+int gemm_planned(int epi, const GemmArgs& a) {
+  const char* why = "";
+  return gemm_shape_ok(epi, a, 2, &why) && xl_usable(epi, a) ? gemm_pick(epi, a) : -1;
+}
+
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
   const char* why = "";
@@ -883,20 +909,12 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     exit(1);
   }
   if constexpr (sizeof(T) == 2) {
-    const size_t abytes = (size_t)a.M * a.lda * sizeof(T), wbytes = (size_t)a.N * a.ldw * sizeof(T);
-    // 16-byte epilogue stores need N, the row strides and the output bases in multiples of 8 elements
-    const bool aligned = a.N % 8 == 0 && ((epi == EPI_STORE || epi == EPI_GEGLU) ? a.ldc % 8 == 0 : true) &&
-                         (epi == EPI_RESID ? a.ldx % 4 == 0 : true) && (epi == EPI_QKV ? a.ldqk % 8 == 0 && a.ldv % 8 == 0 : true);
-    const bool xl_ok = aligned && abytes < (1u << 31) - 65536 && wbytes < (1u << 31) - 65536;
-    if (xl_ok) {
-      // LAYA_GEMM_CFG=0..4 pins one tile configuration (256x256, 256x128, 128x256, 128x128,
-      // 192x256); QKV tiles must not straddle the q/k/v sections and need BM <= BN (RoPE tables in
-      // one stage)
-      const int forced = gemm_pinned();
-      const int D = a.H * a.HD;
-      int cfg = forced >= 0 ? forced : gemm_pick(a.M, a.N, epi, D);
-      if (epi == EPI_QKV && cfg >= 0 && (kXl[cfg].bm > kXl[cfg].bn || D % kXl[cfg].bn))
-        cfg = gemm_pick(a.M, a.N, epi, D);               // a pinned shape QKV cannot use
+    if (xl_usable(epi, a)) {
+      // a pinned configuration (LAYA_GEMM_CFG / gemm_config) wins over the caller's, which wins
+      // over the planner's; a configuration this shape cannot use falls through to the next
+      int cfg = gemm_pinned();
+      if (!xl_cfg_fits(epi, a, cfg)) cfg = a.cfg;
+      if (!xl_cfg_fits(epi, a, cfg)) cfg = gemm_pick(epi, a);
       switch (cfg) {
         case -1: break;
         case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;

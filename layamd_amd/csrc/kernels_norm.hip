@@ -32,8 +32,10 @@ template <> struct St4<bf16_t> {
   }
 };
 
-// Each wave normalises RPW rows; all of their loads are issued before the first reduction so
-// every lane keeps 4*RPW 16-byte loads in flight.
+// Each wave normalises RPW rows.  Every load the wave needs (its rows, then the weight and bias
+// chunks) is issued before the first reduction, so the only latency on a wave's path is one memory
+// round trip followed by the two shuffle reductions per row.  Rows past the end of the batch load
+// the last row again (their stores are skipped), which keeps every wave's reductions uniform.
 template <typename Tin, typename T, int RPW, int NCH>
 __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows, int D,
                                                    float eps, const float* __restrict__ w, const float* __restrict__ b,
@@ -42,51 +44,63 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
                                                    T* __restrict__ yT) {
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;
   const int nc = D >> 2;
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 v[RPW][NCH];
-  float s[RPW];
 #pragma unroll
   for (int q = 0; q < RPW; q++) {
-    s[q] = 0.f;
-    const int row = row0 + q;
-    if (row >= rows) continue;
+    const int row = min(row0 + q, rows - 1);
     const size_t src = gather ? (size_t)gather[row] : (size_t)row;
     const Tin* xr = x + src * D;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
-      if (c < nc) v[q][j] = Ld4<Tin>::at(xr, c);
+      v[q][j] = c < nc ? Ld4<Tin>::at(xr, c) : zero;
     }
   }
+  float4 ww[NCH], bb[NCH];
 #pragma unroll
-  for (int q = 0; q < RPW; q++)
+  for (int j = 0; j < NCH; j++) {
+    const int c = lane + 64 * j;
+    ww[j] = c < nc ? reinterpret_cast<const float4*>(w)[c] : zero;
+    bb[j] = b && c < nc ? reinterpret_cast<const float4*>(b)[c] : zero;
+  }
+  float mean[RPW], inv[RPW];
+#pragma unroll
+  for (int q = 0; q < RPW; q++) {
+    float s = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; j++)
-      if (lane + 64 * j < nc) s[q] += (v[q][j].x + v[q][j].y) + (v[q][j].z + v[q][j].w);
+      if (lane + 64 * j < nc) s += (v[q][j].x + v[q][j].y) + (v[q][j].z + v[q][j].w);
+    mean[q] = wave_sum(s) / D;
+  }
+#pragma unroll
+  for (int q = 0; q < RPW; q++) {
+    float qq = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      if (lane + 64 * j < nc) {
+        const float a = v[q][j].x - mean[q], bq = v[q][j].y - mean[q], cq = v[q][j].z - mean[q],
+                    d = v[q][j].w - mean[q];
+        qq += (a * a + bq * bq) + (cq * cq + d * d);
+      }
+    }
+    inv[q] = rsqrtf(wave_sum(qq) / D + eps);
+  }
 #pragma unroll
   for (int q = 0; q < RPW; q++) {
     const int row = row0 + q;
     if (row >= rows) break;
-    const float mean = wave_sum(s[q]) / D;
-    float qq = 0.f;
-#pragma unroll
-    for (int j = 0; j < NCH; j++) {
-      const int c = lane + 64 * j;
-      if (c < nc) {
-        const float a = v[q][j].x - mean, bb = v[q][j].y - mean, cc = v[q][j].z - mean, d = v[q][j].w - mean;
-        qq += (a * a + bb * bb) + (cc * cc + d * d);
-      }
-    }
-    const float inv = rsqrtf(wave_sum(qq) / D + eps);
     const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
       if (c < nc) {
-        const float4 ww = reinterpret_cast<const float4*>(w)[c];
-        float4 o = make_float4((v[q][j].x - mean) * inv * ww.x, (v[q][j].y - mean) * inv * ww.y,
-                               (v[q][j].z - mean) * inv * ww.z, (v[q][j].w - mean) * inv * ww.w);
-        if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
+        const float4 ww4 = ww[j];
+        float4 o = make_float4((v[q][j].x - mean[q]) * inv[q] * ww4.x, (v[q][j].y - mean[q]) * inv[q] * ww4.y,
+                               (v[q][j].z - mean[q]) * inv[q] * ww4.z, (v[q][j].w - mean[q]) * inv[q] * ww4.w);
+        if (b) { o.x += bb[j].x; o.y += bb[j].y; o.z += bb[j].z; o.w += bb[j].w; }
         if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
         if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
         if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
@@ -95,19 +109,20 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
   }
 }
 
+// One row per wave: a 1024-wide row is 4 KiB of fp32, and with one row per wave every workgroup
+// of the launch is resident at once (about 2400 workgroups for 9.5k rows), which measured faster
+// than two or four rows per wave (fewer, longer waves).
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
                       const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st) {
   if (D % 4 || D > kLnMaxChunks * 256) { fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D); exit(1); }
   if (rows <= 0) return;
-  if (D <= 1024) {
-    constexpr int RPW = 2;
-    hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x, gather,
-                       rows, D, eps, w, b, addtab, qt, seq, y32, yT);
-  } else {
-    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
-                       addtab, qt, seq, y32, yT);
-  }
+  if (D <= 1024)
+    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, 4>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps,
+                       w, b, addtab, qt, seq, y32, yT);
+  else
+    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows,
+                       D, eps, w, b, addtab, qt, seq, y32, yT);
 }
 
 template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
@@ -116,6 +131,26 @@ template void launch_layernorm<float, bf16_t>(const float*, const int*, int, int
                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
 template void launch_layernorm<bf16_t, bf16_t>(const bf16_t*, const int*, int, int, float, const float*, const float*,
                                                const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
+
+// Deterministic finite pattern, uniform in [-1, 1), written over n elements (operands for GEMM
+// tuning runs, which must see realistic MFMA power and produce finite results).
+template <typename T>
+__global__ __launch_bounds__(256) void k_fill_pattern(T* __restrict__ p, size_t n, uint32_t seed) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    uint32_t h = (uint32_t)i * 0x9E3779B1u ^ seed;
+    h ^= h >> 16; h *= 0x7FEB352Du; h ^= h >> 15; h *= 0x846CA68Bu; h ^= h >> 16;
+    Elt<T>::st(p + i, (float)(h >> 8) * (2.0f / 16777216.0f) - 1.0f);
+  }
+}
+
+template <typename T>
+void launch_fill_pattern(T* p, size_t n, uint32_t seed, hipStream_t st) {
+  if (n == 0) return;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_fill_pattern<T>, dim3((unsigned)blocks), dim3(256), 0, st, p, n, seed);
+}
+template void launch_fill_pattern<float>(float*, size_t, uint32_t, hipStream_t);
+template void launch_fill_pattern<bf16_t>(bf16_t*, size_t, uint32_t, hipStream_t);
 
 __global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, const int* __restrict__ rows,
                                                      float* __restrict__ xg, int R, int D) {

@@ -311,6 +311,25 @@ def test_tile_configs_bit_identical():
     assert np.isfinite(ref_lo).all() and np.isfinite(ref_ac).all()
 
 
+def test_gemm_tuning_keeps_outputs():
+    """laya_tune_all times every tile configuration of every GEMM bucket up to the pass capacity, as
+    the reference tunes its GEMM plans per M bucket (src/engine.hip:295-379).  All configurations
+    give bit-identical results, so a tuned engine and one running the analytic planner only
+    (LAYA_TUNE=0) agree exactly, before and after tune_all."""
+    import time
+    b = wl.c3(0).subset(list(range(8)))
+    lo0, ac0 = engine("large", "bf16", LAYA_TUNE=0).forward_flat(*b.flat())
+    e = engine("large", "bf16", LAYA_MAX_TOKENS=8192)
+    lo1, ac1 = e.forward_flat(*b.flat())
+    t0 = time.time()
+    e.tune_all()
+    print("tune_all over 8192 rows: %.2f s" % (time.time() - t0))
+    lo2, ac2 = e.forward_flat(*b.flat())
+    assert np.isfinite(lo0).all() and np.isfinite(ac0).all()
+    for lo, ac in ((lo1, ac1), (lo2, ac2)):
+        assert np.array_equal(lo, lo0) and np.array_equal(ac, ac0)
+
+
 def test_large_bf16_c3_sample_vs_oracle():
     """Four questions of the bf16 b32 x s512 benchmark batch against the fp32 CPU oracle."""
     import torch
