@@ -41,6 +41,12 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
  * previous setting, or -2 for an invalid value. */
 int laya_ext_gemm_config(int cfg);
 
+/* Row split used with the pinned configuration: rows [split_rows, M) of every later pinned launch
+ * run as a second launch with tile configuration cfg_tail (0..4); split_rows 0 removes the split.
+ * A split the shape cannot take (split_rows >= M, not a multiple of 8, a tail configuration the
+ * shape cannot use) runs as one launch.  Returns 0, or -2 for an invalid value. */
+int laya_ext_gemm_split(int split_rows, int cfg_tail);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,14 +50,15 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + er
 // The same erf GELU with erf from Abramowitz & Stegun, Handbook of Mathematical Functions, formula
 // 7.1.26: erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2), t = 1 / (1 + p z),
 // z >= 0, |error| <= 1.5e-7.  Used where the result is rounded to bf16 (2^-9 relative), about a
-// quarter of the instructions of the library erff.
+// quarter of the instructions of the library erff.  z = |x| / sqrt(2) is folded into the
+// constants: p z = (p / sqrt 2) |x| and exp(-z^2) = 2^(-x^2 log2(e) / 2); the result is
+// x (1/2 + erf / 2) with the sign of x on the erf term.
 __device__ __forceinline__ float gelu_erf_as(float x) {
-  const float z = fabsf(x) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752440f, fabsf(x), 1.0f));
   const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f),
                               0.254829592f);
-  const float e = 1.0f - poly * __expf(-z * z);
-  return 0.5f * x * (1.0f + copysignf(e, x));
+  const float e = fmaf(-poly, __builtin_amdgcn_exp2f(x * x * -0.72134752044448170368f), 1.0f);
+  return x * fmaf(0.5f, copysignf(e, x), 0.5f);
 }
 
 }  // namespace laya

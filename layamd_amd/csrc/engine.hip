@@ -137,7 +137,11 @@ struct Engine : EngineIface {
   // measured bf16 tile configuration per (epilogue, activation, N, K, RoPE, M bucket), filled before
   // the first pass of a shape (or by tune_all); every configuration gives bit-identical results
   using TuneKey = std::tuple<int, int, int, int, int, int>;
-  std::map<TuneKey, int> tuned;
+  // a tuned launch: tile configuration, and optionally the first `split_tiles` tile rows in it and
+  // the remaining rows in a second launch with configuration `tail`
+  struct TilePlan { int cfg = -1, split_tiles = 0, tail = -1; };
+  std::map<TuneKey, TilePlan> tuned;
+  int n_cu = 256;
   std::set<Shape> tuned_shapes;
   bool tune_on = true;
   std::vector<std::pair<int, GemmArgs>>* collecting = nullptr;   // set while a pass's GEMMs are listed
@@ -323,6 +327,11 @@ struct Engine : EngineIface {
     d_gtiles = dalloc<AttnTile>(caps.gtiles); h_gtiles = halloc<AttnTile>(caps.gtiles);
 
     LAYA_HIP(hipStreamCreate(&stream));
+    {
+      int dev = 0;
+      LAYA_HIP(hipGetDevice(&dev));
+      LAYA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    }
     prof.init();
     use_graphs = env_int("LAYA_GRAPHS", 1) != 0;
     tune_on = env_int("LAYA_TUNE", 1) != 0;
@@ -377,28 +386,53 @@ struct Engine : EngineIface {
   void gemm(int epi, GemmArgs g, hipStream_t st) {
     if (collecting) { collecting->emplace_back(epi, g); return; }
     auto it = tuned.find(tune_key(epi, g));
-    if (it != tuned.end()) g.cfg = it->second;
+    if (it != tuned.end()) apply_plan(g, it->second);
     launch_gemm<T>(epi, g, st);
+  }
+
+  static void apply_plan(GemmArgs& g, const TilePlan& p) {
+    g.cfg = p.cfg;
+    const int rows = p.split_tiles * gemm_config_bm(p.cfg);
+    if (p.split_tiles > 0 && rows < g.M) { g.split_rows = rows; g.cfg_tail = p.tail; }
+    else { g.split_rows = 0; g.cfg_tail = -1; }
   }
 
   // Times every tile configuration this GEMM can use, at its own M, on its own buffers (which hold
   // nothing live before a pass), and returns the fastest: the analytic pick unless another one is
-  // more than 3% faster.  The operand rows are first filled with a finite pattern so the timing
-  // sees realistic MFMA power and the V^T rows a QKV candidate writes stay finite.
-  int tune_gemm(int epi, GemmArgs g) {
-    const int first = gemm_planned(epi, g);
-    if (first < 0) return -1;
+  // more than 3% faster.  Besides single launches, the candidates include row splits: large tiles
+  // over the rows that fill whole rounds of the CUs (the last one, or the last two), and 128x128
+  // or 128x256 tiles over the rest, so that a partial last round of large tiles is not paid in
+  // full.  The operand rows are first filled with a finite pattern so the timing sees realistic
+  // MFMA power and the V^T rows a QKV candidate writes stay finite.
+  TilePlan tune_gemm(int epi, GemmArgs g) {
+    TilePlan first;
+    first.cfg = gemm_planned(epi, g);
+    if (first.cfg < 0) return first;
+    std::vector<TilePlan> cands = {first};
+    for (int c = 0; c < kGemmConfigs; c++)
+      if (c != first.cfg && gemm_config_valid(epi, g, c)) cands.push_back(TilePlan{c, 0, -1});
+    for (int c1 : {0, 4}) {
+      if (!gemm_config_valid(epi, g, c1)) continue;
+      const int bm = gemm_config_bm(c1), tn = (g.N + gemm_config_bn(c1) - 1) / gemm_config_bn(c1);
+      const int rounds = ((g.M + bm - 1) / bm) * tn / n_cu;
+      int last_kb = -1;
+      for (int r = rounds; r >= std::max(1, rounds - 1); r--) {
+        const int kb = r * n_cu / tn;
+        if (kb < 1 || kb == last_kb || kb * bm >= g.M) continue;
+        last_kb = kb;
+        for (int c2 : {3, 2})
+          if (gemm_split_valid(epi, g, c1, kb * bm, c2)) cands.push_back(TilePlan{c1, kb, c2});
+      }
+    }
     launch_fill_pattern((T*)const_cast<void*>(g.A), (size_t)g.M * g.lda, 0x9E3779B9u ^ (uint32_t)g.K, stream);
     hipEvent_t a, b;
     LAYA_HIP(hipEventCreate(&a));
     LAYA_HIP(hipEventCreate(&b));
     const int reps = g.M >= 2048 ? 3 : 8;
-    int best = first;
+    TilePlan best = first;
     float bt = 1e30f;
-    for (int i = -1; i < kGemmConfigs; i++) {
-      const int c = i < 0 ? first : i;
-      if ((i >= 0 && c == first) || !gemm_config_valid(epi, g, c)) continue;
-      g.cfg = c;
+    for (const TilePlan& p : cands) {
+      apply_plan(g, p);
       launch_gemm<T>(epi, g, stream);
       LAYA_HIP(hipEventRecord(a, stream));
       for (int r = 0; r < reps; r++) launch_gemm<T>(epi, g, stream);
@@ -407,8 +441,10 @@ struct Engine : EngineIface {
       float ms = 0.f;
       LAYA_HIP(hipEventElapsedTime(&ms, a, b));
       ms /= reps;
-      if (verbose) printf("[laya] tune epi %d %5dx%5dx%5d cfg %d: %8.1f us\n", epi, g.M, g.N, g.K, c, ms * 1e3f);
-      if (ms < bt * 0.97f) { bt = ms; best = c; }
+      if (verbose)
+        printf("[laya] tune epi %d %5dx%5dx%5d cfg %d split %5d tail %2d: %8.1f us\n", epi, g.M, g.N, g.K, p.cfg,
+               g.split_rows, g.cfg_tail, ms * 1e3f);
+      if (ms < bt * 0.97f) { bt = ms; best = p; }
     }
     LAYA_HIP(hipEventDestroy(a));
     LAYA_HIP(hipEventDestroy(b));
@@ -714,7 +750,12 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
 }
 const char* laya_ext_precision(void* h) { return E(h)->precision(); }
 int laya_ext_gemm_config(int cfg) {
-  if (cfg < -1 || cfg > 4) return -2;
+  if (cfg < -1 || cfg >= laya::kGemmConfigs) return -2;
   return laya::gemm_config(cfg);
+}
+int laya_ext_gemm_split(int split_rows, int cfg_tail) {
+  if (split_rows < 0 || (split_rows > 0 && (cfg_tail < 0 || cfg_tail >= laya::kGemmConfigs))) return -2;
+  laya::gemm_pin_split(split_rows, split_rows > 0 ? cfg_tail : -1);
+  return 0;
 }
 }

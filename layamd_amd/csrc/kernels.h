@@ -41,6 +41,9 @@ struct GemmArgs {
   const int* pos = nullptr;                      // RoPE position of each row
   const float* rope_cos = nullptr; const float* rope_sin = nullptr;  // [positions][HD/2]
   int cfg = -1;                                  // bf16 tile configuration (-1: the planner's pick)
+  // rows [split_rows, M) run as a second launch with configuration cfg_tail (0: one launch); the
+  // first launch then covers whole rounds of large tiles and the second the few rows left over
+  int split_rows = 0, cfg_tail = -1;
 };
 
 template <typename T>
@@ -50,10 +53,17 @@ bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
 // 128x256, 128x128, 192x256); returns the previous setting
 int gemm_config(int cfg);
 int gemm_pinned();                               // the pinned configuration, or -1
+// row split used together with the pinned configuration: rows [split_rows, M) run as a second
+// launch with cfg_tail (split_rows 0: none)
+void gemm_pin_split(int split_rows, int cfg_tail);
 constexpr int kGemmConfigs = 5;
 // whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
 // shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)
 bool gemm_config_valid(int epi, const GemmArgs& a, int cfg);
+bool gemm_split_valid(int epi, const GemmArgs& a, int cfg, int split_rows, int cfg_tail);
+// tile rows and columns of configuration cfg (0 for an invalid cfg)
+int gemm_config_bm(int cfg);
+int gemm_config_bn(int cfg);
 int gemm_planned(int epi, const GemmArgs& a);
 
 // ---- attention over packed sequences ----

@@ -492,7 +492,7 @@ __device__ __forceinline__ void xl_k_loop(f32x16_t (&acc)[FM][FN], ST& S0, ST& S
   LAYA_WAIT_VMCNT(0);                                            // the refills past the last slice
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, int ACT>
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -515,6 +515,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // all tiles use the transposed product except the V columns of the QKV projection, which are
   // stored transposed themselves (V^T) and keep the direct one
   const bool swap = EPI == EPI_QKV ? n0 < 2 * D : true;
+
+  // RoPE positions of the rows whose table pieces this thread stages in the QKV epilogue, loaded
+  // first so that they are the oldest loads (the K loop's counted waits then never wait on them)
+  // and the epilogue can issue its table loads at once
+  constexpr int NT = BM * 8 / 256;
+  int pp[EPI == EPI_QKV ? NT : 1];
+  if constexpr (EPI == EPI_QKV) {
+    if (swap && a.rope_cos != nullptr) {
+#pragma unroll
+      for (int k = 0; k < NT; k++) pp[k] = a.pos[min(m0 + ((tid + 256 * k) >> 3), a.M - 1)];
+    }
+  }
 
   XlDma<PA, PB> dm;
   dm.rA = make_rsrc(a.A, (uint32_t)((size_t)a.M * a.lda * sizeof(T)));
@@ -615,14 +627,19 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // widest power-of-two column count <= cap that divides w
   constexpr auto fitw = [](int w, int cap) { int c = w & -w; while (c > cap) c /= 2; return c; };
 
+  // the bias loads and adds exist only in the kernels for GEMMs that have a bias (HB)
+  auto ab = [](float v, float b) {
+    if constexpr (HB) return v + b;
+    else return v;
+  };
   if constexpr (EPI == EPI_RESID) {
     // fp32: blocks of 32 rows x CW columns
     constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
-    float4 bb[FN][4];
+    float4 bb[FN][4] = {};
 #pragma unroll
     for (int j = 0; j < FN; j++)
 #pragma unroll
-      for (int g = 0; g < 4; g++) bb[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+      for (int g = 0; g < 4; g++) if constexpr (HB) bb[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -632,10 +649,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
           for (int g = 0; g < 4; g++) {
             float4 v;
-            v.x = acc[i][j][4 * g + 0] + bb[j][g].x;
-            v.y = acc[i][j][4 * g + 1] + bb[j][g].y;
-            v.z = acc[i][j][4 * g + 2] + bb[j][g].z;
-            v.w = acc[i][j][4 * g + 3] + bb[j][g].w;
+            v.x = ab(acc[i][j][4 * g + 0], bb[j][g].x);
+            v.y = ab(acc[i][j][4 * g + 1], bb[j][g].y);
+            v.z = ab(acc[i][j][4 * g + 2], bb[j][g].z);
+            v.w = ab(acc[i][j][4 * g + 3], bb[j][g].w);
             *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
           }
         const int c0 = cbase + cp * CW;
@@ -650,11 +667,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     constexpr int CW = fitw(OW, SB / 64), CPR = CW / 8;
     const int ocol = EPI == EPI_GEGLU ? cbase / 2 : cbase, ncol = EPI == EPI_GEGLU ? a.N / 2 : a.N;
     // bias per (column block, e / 4): input and gate parts for GeGLU
-    float4 bx[FN][4];
+    float4 bx[FN][4] = {};
 #pragma unroll
     for (int j = 0; j < FN; j++)
 #pragma unroll
-      for (int g = 0; g < 4; g++) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+      for (int g = 0; g < 4; g++) if constexpr (HB) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
     auto f = [](float v) {
       if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
       if constexpr (ACT == ACT_GELU) v = gelu_erf_as(v);
@@ -669,8 +686,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
-              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(acc[i][j][4 * g + 0] + bx[j][g].x),
-                   f(acc[i][j][4 * g + 1] + bx[j][g].y), f(acc[i][j][4 * g + 2] + bx[j][g].z), f(acc[i][j][4 * g + 3] + bx[j][g].w));
+              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(ab(acc[i][j][4 * g + 0], bx[j][g].x)),
+                   f(ab(acc[i][j][4 * g + 1], bx[j][g].y)), f(ab(acc[i][j][4 * g + 2], bx[j][g].z)), f(ab(acc[i][j][4 * g + 3], bx[j][g].w)));
         } else {
           // 64-column groups [input 32 | gate 32] (blocks jp, jp + 1) -> output column (c / 64) * 32 + c % 64
 #pragma unroll
@@ -680,9 +697,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
               const float4 x = bx[jp][g], y = bx[jp + 1][g];
               const f32x16_t& p = acc[i][jp];
               const f32x16_t& q = acc[i][jp + 1];
-              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(p[4 * g + 0] + x.x) * (q[4 * g + 0] + y.x),
-                   gelu_erf_as(p[4 * g + 1] + x.y) * (q[4 * g + 1] + y.y), gelu_erf_as(p[4 * g + 2] + x.z) * (q[4 * g + 2] + y.z),
-                   gelu_erf_as(p[4 * g + 3] + x.w) * (q[4 * g + 3] + y.w));
+              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(ab(p[4 * g + 0], x.x)) * ab(q[4 * g + 0], y.x),
+                   gelu_erf_as(ab(p[4 * g + 1], x.y)) * ab(q[4 * g + 1], y.y), gelu_erf_as(ab(p[4 * g + 2], x.z)) * ab(q[4 * g + 2], y.z),
+                   gelu_erf_as(ab(p[4 * g + 3], x.w)) * ab(q[4 * g + 3], y.w));
             }
         }
         const int c0 = ocol + cp * CW;
@@ -699,12 +716,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       float* tcos = reinterpret_cast<float*>(&S0);
       float* tsin = reinterpret_cast<float*>(&S1);
       if (rope) {
-        // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each):
-        // position loads first, then the table loads, four 16-byte pieces per thread at a time
-        constexpr int NT = BM * 8 / 256;
-        int pp[NT];
-#pragma unroll
-        for (int k = 0; k < NT; k++) pp[k] = a.pos[min(m0 + ((tid + 256 * k) >> 3), a.M - 1)];
+        // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
+        // four 16-byte pieces per thread at a time (the positions were loaded before the K loop)
 #pragma unroll
         for (int k0 = 0; k0 < NT; k0 += 4) {
           float4 tc[4], ts[4];
@@ -722,11 +735,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           }
         }
       }
-      float4 bx[FN][4];
+      float4 bx[FN][4] = {};
 #pragma unroll
       for (int j = 0; j < FN; j++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+        for (int g = 0; g < 4; g++) if constexpr (HB) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
       if (rope) __syncthreads();                          // tables complete
       T* dst = reinterpret_cast<T*>(cbase < D ? a.Q : a.Kt) + (cbase % D);
 #pragma unroll
@@ -740,10 +753,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
             for (int g = 0; g < 4; g++) {
               const int dd = 8 * g + 4 * hi;
               const float4 x0 = bx[jp][g], x1 = bx[jp + 1][g];
-              const float p1[4] = {acc[i][jp][4 * g + 0] + x0.x, acc[i][jp][4 * g + 1] + x0.y, acc[i][jp][4 * g + 2] + x0.z,
-                                   acc[i][jp][4 * g + 3] + x0.w};
-              const float p2[4] = {acc[i][jp + 1][4 * g + 0] + x1.x, acc[i][jp + 1][4 * g + 1] + x1.y,
-                                   acc[i][jp + 1][4 * g + 2] + x1.z, acc[i][jp + 1][4 * g + 3] + x1.w};
+              const float p1[4] = {ab(acc[i][jp][4 * g + 0], x0.x), ab(acc[i][jp][4 * g + 1], x0.y), ab(acc[i][jp][4 * g + 2], x0.z),
+                                   ab(acc[i][jp][4 * g + 3], x0.w)};
+              const float p2[4] = {ab(acc[i][jp + 1][4 * g + 0], x1.x), ab(acc[i][jp + 1][4 * g + 1], x1.y),
+                                   ab(acc[i][jp + 1][4 * g + 2], x1.z), ab(acc[i][jp + 1][4 * g + 3], x1.w)};
               float o1[4], o2[4];
               if (rope) {
                 // rotate_half partners (d, d + 32) of a head are blocks jp, jp + 1 of one lane
@@ -775,15 +788,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < FN; j++) {
         const int n = cbase + j * 32 + l32;
-        const float bv = (a.bias && n < a.N) ? a.bias[n] : 0.f;
+        const float bv = HB && a.bias && n < a.N ? a.bias[n] : 0.f;
 #pragma unroll
         for (int cp = 0; cp < WTM / CW; cp++) {
 #pragma unroll
           for (int i = cp * CW / 32; i < (cp + 1) * CW / 32; i++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
-              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, acc[i][j][4 * g + 0] + bv, acc[i][j][4 * g + 1] + bv,
-                   acc[i][j][4 * g + 2] + bv, acc[i][j][4 * g + 3] + bv);
+              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, ab(acc[i][j][4 * g + 0], bv), ab(acc[i][j][4 * g + 1], bv),
+                   ab(acc[i][j][4 * g + 2], bv), ab(acc[i][j][4 * g + 3], bv));
           const int r0 = rbase + cp * CW;
           flush(CPR, [&](int rr) -> char* {
             const int nn = cbase + j * 32 + rr;
@@ -795,22 +808,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   }
 }
 
+// GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
+// build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
+template <int BM, int BN, int WM, int WN, int EPI, int ACT>
+static void launch_xl_hb(const GemmArgs& a, hipStream_t st) {
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true>), dim3(tiles), dim3(256), 0, st, a);
+  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false>), dim3(tiles), dim3(256), 0, st, a);
+}
+
 template <int BM, int BN, int WM, int WN>
 static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
-  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (epi == EPI_STORE) {
-    if (a.act == ACT_RELU) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_RELU>), dim3(tiles), dim3(256), 0, st, a);
-    else if (a.act == ACT_GELU) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_GELU>), dim3(tiles), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_STORE, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a);
+    if (a.act == ACT_RELU) launch_xl_hb<BM, BN, WM, WN, EPI_STORE, ACT_RELU>(a, st);
+    else if (a.act == ACT_GELU) launch_xl_hb<BM, BN, WM, WN, EPI_STORE, ACT_GELU>(a, st);
+    else launch_xl_hb<BM, BN, WM, WN, EPI_STORE, ACT_NONE>(a, st);
     return;
   }
   switch (epi) {
-    case EPI_RESID: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_RESID, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_RESID: launch_xl_hb<BM, BN, WM, WN, EPI_RESID, ACT_NONE>(a, st); break;
     case EPI_QKV:
-      if constexpr (BM <= BN) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_QKV, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a);
+      if constexpr (BM <= BN) launch_xl_hb<BM, BN, WM, WN, EPI_QKV, ACT_NONE>(a, st);
       else { fprintf(stderr, "[laya] gemm: QKV tiles need BM <= BN\n"); exit(1); }
       break;
-    case EPI_GEGLU: hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI_GEGLU, ACT_NONE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_GEGLU: launch_xl_hb<BM, BN, WM, WN, EPI_GEGLU, ACT_NONE>(a, st); break;
     default: fprintf(stderr, "[laya] gemm: bad epilogue %d\n", epi); exit(1);
   }
 }
@@ -846,6 +867,14 @@ int gemm_config(int cfg) {
   const int prev = gemm_pinned();
   g_gemm_cfg.store(cfg, std::memory_order_relaxed);
   return prev;
+}
+
+// row split applied with the pinned configuration (0: none)
+static std::atomic<int> g_split_rows{0}, g_cfg_tail{-1};
+
+void gemm_pin_split(int split_rows, int cfg_tail) {
+  g_split_rows.store(split_rows, std::memory_order_relaxed);
+  g_cfg_tail.store(cfg_tail, std::memory_order_relaxed);
 }
 
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) {
@@ -896,9 +925,47 @@ bool gemm_config_valid(int epi, const GemmArgs& a, int cfg) {
   return gemm_shape_ok(epi, a, 2, &why) && xl_usable(epi, a) && xl_cfg_fits(epi, a, cfg);
 }
 
+int gemm_config_bm(int cfg) { return cfg >= 0 && cfg < kGemmConfigs ? kXl[cfg].bm : 0; }
+int gemm_config_bn(int cfg) { return cfg >= 0 && cfg < kGemmConfigs ? kXl[cfg].bn : 0; }
+
+// the same GEMM restricted to rows [r0, M): every row-indexed operand moves by r0 rows (V^T by r0
+// columns); the K order of every output element is unchanged
+static GemmArgs rows_from(const GemmArgs& a, int r0) {
+  GemmArgs b = a;
+  b.M = a.M - r0;
+  b.A = reinterpret_cast<const bf16_t*>(a.A) + (size_t)r0 * a.lda;
+  if (a.C) b.C = reinterpret_cast<bf16_t*>(a.C) + (size_t)r0 * a.ldc;
+  if (a.X) b.X = a.X + (size_t)r0 * a.ldx;
+  if (a.Q) b.Q = reinterpret_cast<bf16_t*>(a.Q) + (size_t)r0 * a.ldqk;
+  if (a.Kt) b.Kt = reinterpret_cast<bf16_t*>(a.Kt) + (size_t)r0 * a.ldqk;
+  if (a.Vt) b.Vt = reinterpret_cast<bf16_t*>(a.Vt) + r0;
+  if (a.pos) b.pos = a.pos + r0;
+  b.split_rows = 0;
+  return b;
+}
+
+bool gemm_split_valid(int epi, const GemmArgs& a, int cfg, int split_rows, int cfg_tail) {
+  // 8-row multiples keep the moved V^T columns 16-byte aligned
+  if (split_rows <= 0 || split_rows >= a.M || split_rows % 8) return false;
+  GemmArgs head = a;
+  head.M = split_rows;
+  return gemm_config_valid(epi, head, cfg) && gemm_config_valid(epi, rows_from(a, split_rows), cfg_tail);
+}
+
 int gemm_planned(int epi, const GemmArgs& a) {
   const char* why = "";
   return gemm_shape_ok(epi, a, 2, &why) && xl_usable(epi, a) ? gemm_pick(epi, a) : -1;
+}
+
+static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
+  switch (cfg) {
+    case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;
+    case 1: launch_xl<256, 128, 2, 2>(epi, a, st); return;
+    case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
+    case 3: launch_xl<128, 128, 2, 2>(epi, a, st); return;
+    case 4: launch_xl<192, 256, 2, 2>(epi, a, st); return;
+    default: fprintf(stderr, "[laya] gemm: bad tile configuration %d\n", cfg); exit(1);
+  }
 }
 
 template <typename T>
@@ -910,19 +977,24 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
   }
   if constexpr (sizeof(T) == 2) {
     if (xl_usable(epi, a)) {
-      // a pinned configuration (LAYA_GEMM_CFG / gemm_config) wins over the caller's, which wins
-      // over the planner's; a configuration this shape cannot use falls through to the next
-      int cfg = gemm_pinned();
-      if (!xl_cfg_fits(epi, a, cfg)) cfg = a.cfg;
-      if (!xl_cfg_fits(epi, a, cfg)) cfg = gemm_pick(epi, a);
-      switch (cfg) {
-        case -1: break;
-        case 0: launch_xl<256, 256, 2, 2>(epi, a, st); return;
-        case 1: launch_xl<256, 128, 2, 2>(epi, a, st); return;
-        case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
-        case 4: launch_xl<192, 256, 2, 2>(epi, a, st); return;
-        default: launch_xl<128, 128, 2, 2>(epi, a, st); return;
+      // a pinned configuration (LAYA_GEMM_CFG / gemm_config, with its pinned row split) wins over
+      // the caller's, which wins over the planner's; one this shape cannot use falls through
+      int cfg = a.cfg, split = a.split_rows, tail = a.cfg_tail;
+      const int pinned = gemm_pinned();
+      if (xl_cfg_fits(epi, a, pinned)) {
+        cfg = pinned;
+        split = g_split_rows.load(std::memory_order_relaxed);
+        tail = g_cfg_tail.load(std::memory_order_relaxed);
       }
+      if (split > 0 && gemm_split_valid(epi, a, cfg, split, tail)) {
+        GemmArgs head = a;
+        head.M = split;
+        launch_xl_cfg(epi, head, cfg, st);
+        launch_xl_cfg(epi, rows_from(a, split), tail, st);
+        return;
+      }
+      if (!xl_cfg_fits(epi, a, cfg)) cfg = gemm_pick(epi, a);
+      if (cfg >= 0) { launch_xl_cfg(epi, a, cfg, st); return; }
     }
   }
   launch_cfg<T, 128, 128, 2, 2>(epi, a, st);

@@ -78,6 +78,20 @@ def test_gemm_vs_torch(dtype, cfg, M, N, K):
         le.gemm_config(lib, prev)
 
 
+# row splits: rows [split, M) in a second launch with another tile shape (split >= M: one launch)
+@pytest.mark.parametrize("cfg,split,tail", [(0, 256, 3), (4, 192, 2), (3, 128, 1), (0, 264, 4)])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 192), (513, 1024, 2624), (200, 256, 320)])
+def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
+    lib = le.load_library()
+    prev = le.gemm_config(lib, cfg)
+    le.gemm_split(lib, split, tail)
+    try:
+        _check_gemm(lib, "bf16", M, N, K)
+    finally:
+        le.gemm_split(lib, 0)
+        le.gemm_config(lib, prev)
+
+
 def _check_gemm(lib, dtype, M, N, K):
     import torch
     g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
@@ -296,7 +310,8 @@ def test_large_bf16_c1_drift():
 def test_tile_configs_bit_identical():
     """Every bf16 tile configuration runs the same K order through the same MFMA instruction, so the
     whole pass (all 28 layers of ModernBERT-large, 32 questions of the b32 x s512 batch, split into
-    two passes) must give bit-identical outputs whichever tiles the GEMMs use."""
+    two passes) must give bit-identical outputs whichever tiles the GEMMs use, also when a GEMM's
+    rows are split over two launches with different tiles."""
     e = engine("large", "bf16", LAYA_GRAPHS=0)
     b = wl.c3(0)
     prev = le.gemm_config(e.lib, -1)
@@ -306,7 +321,14 @@ def test_tile_configs_bit_identical():
             le.gemm_config(e.lib, cfg)
             lo, ac = e.forward_flat(*b.flat())
             assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
+        # row splits: large tiles over the first rows, another shape over the rest
+        for cfg, split, tail in ((0, 1024, 3), (4, 960, 2), (0, 4096, 1)):
+            le.gemm_config(e.lib, cfg)
+            le.gemm_split(e.lib, split, tail)
+            lo, ac = e.forward_flat(*b.flat())
+            assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), (cfg, split, tail)
     finally:
+        le.gemm_split(e.lib, 0)
         le.gemm_config(e.lib, prev)
     assert np.isfinite(ref_lo).all() and np.isfinite(ref_ac).all()
 
