@@ -497,13 +497,17 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int PA = BM / 64, PB = BN / 64;              // DMA instructions per wave and slice
-  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0, "tile");
-  // five 32-deep K stages ((BM + BN) * 64 bytes each), separate objects so the compiler sees that
+  // the A part of a stage holds BM rounded up to whole DMA instructions (64 rows over the 4 waves);
+  // rows BM.. of it are fetched (the next tile's rows, or zeros past M) and never read
+  constexpr int BMP = (BM + 63) / 64 * 64;
+  constexpr int PA = BMP / 64, PB = BN / 64;             // DMA instructions per wave and slice
+  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0 && BN % 64 == 0, "tile");
+  // five 32-deep K stages ((BMP + BN) * 64 bytes each), separate objects so the compiler sees that
   // the DMA into one stage and the fragment reads of another never alias
-  struct Stage { u32x4_t a[BM * 4]; u32x4_t b[BN * 4]; };
+  struct Stage { u32x4_t a[BMP * 4]; u32x4_t b[BN * 4]; };
   __shared__ Stage S0, S1, S2, S3, S4;
-  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BM + BN) * 64, "RoPE tables: one stage each for cos and sin");
+  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BMP + BN) * 64, "RoPE tables: one stage each for cos and sin");
+  static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
@@ -723,12 +727,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           float4 tc[4], ts[4];
 #pragma unroll
           for (int k = 0; k < 4; k++) {
+            if (k0 + k >= NT) break;
             const int q = (tid + 256 * (k0 + k)) & 7;
             tc[k] = *reinterpret_cast<const float4*>(a.rope_cos + pp[k0 + k] * 32 + 4 * q);
             ts[k] = *reinterpret_cast<const float4*>(a.rope_sin + pp[k0 + k] * 32 + 4 * q);
           }
 #pragma unroll
           for (int k = 0; k < 4; k++) {
+            if (k0 + k >= NT) break;
             const int it = tid + 256 * (k0 + k), r = it >> 3, q = it & 7;
             *reinterpret_cast<float4*>(tcos + r * 32 + 4 * q) = tc[k];
             *reinterpret_cast<float4*>(tsin + r * 32 + 4 * q) = ts[k];
@@ -764,8 +770,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
                 const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(tsin + r * 32 + dd);
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                  o1[u] = p1[u] * cs[u] - p2[u] * sn[u];
-                  o2[u] = p2[u] * cs[u] + p1[u] * sn[u];
+                  // explicit fused forms: left to contraction, different tile shapes could round
+                  // these differently
+                  o1[u] = fmaf(p1[u], cs[u], -(p2[u] * sn[u]));
+                  o2[u] = fmaf(p2[u], cs[u], p1[u] * sn[u]);
                 }
               } else {
 #pragma unroll

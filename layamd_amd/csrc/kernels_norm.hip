@@ -32,10 +32,8 @@ template <> struct St4<bf16_t> {
   }
 };
 
-// Each wave normalises RPW rows.  Every load the wave needs (its rows, then the weight and bias
-// chunks) is issued before the first reduction, so the only latency on a wave's path is one memory
-// round trip followed by the two shuffle reductions per row.  Rows past the end of the batch load
-// the last row again (their stores are skipped), which keeps every wave's reductions uniform.
+// Each wave normalises RPW rows; all of their loads are issued before the first reduction so
+// every lane keeps 4*RPW 16-byte loads in flight.
 template <typename Tin, typename T, int RPW, int NCH>
 __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows, int D,
                                                    float eps, const float* __restrict__ w, const float* __restrict__ b,
@@ -44,63 +42,51 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
                                                    T* __restrict__ yT) {
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
-  if (row0 >= rows) return;
   const int nc = D >> 2;
-  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 v[RPW][NCH];
+  float s[RPW];
 #pragma unroll
   for (int q = 0; q < RPW; q++) {
-    const int row = min(row0 + q, rows - 1);
+    s[q] = 0.f;
+    const int row = row0 + q;
+    if (row >= rows) continue;
     const size_t src = gather ? (size_t)gather[row] : (size_t)row;
     const Tin* xr = x + src * D;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
-      v[q][j] = c < nc ? Ld4<Tin>::at(xr, c) : zero;
+      if (c < nc) v[q][j] = Ld4<Tin>::at(xr, c);
     }
   }
-  float4 ww[NCH], bb[NCH];
 #pragma unroll
-  for (int j = 0; j < NCH; j++) {
-    const int c = lane + 64 * j;
-    ww[j] = c < nc ? reinterpret_cast<const float4*>(w)[c] : zero;
-    bb[j] = b && c < nc ? reinterpret_cast<const float4*>(b)[c] : zero;
-  }
-  float mean[RPW], inv[RPW];
-#pragma unroll
-  for (int q = 0; q < RPW; q++) {
-    float s = 0.f;
+  for (int q = 0; q < RPW; q++)
 #pragma unroll
     for (int j = 0; j < NCH; j++)
-      if (lane + 64 * j < nc) s += (v[q][j].x + v[q][j].y) + (v[q][j].z + v[q][j].w);
-    mean[q] = wave_sum(s) / D;
-  }
-#pragma unroll
-  for (int q = 0; q < RPW; q++) {
-    float qq = 0.f;
-#pragma unroll
-    for (int j = 0; j < NCH; j++) {
-      if (lane + 64 * j < nc) {
-        const float a = v[q][j].x - mean[q], bq = v[q][j].y - mean[q], cq = v[q][j].z - mean[q],
-                    d = v[q][j].w - mean[q];
-        qq += (a * a + bq * bq) + (cq * cq + d * d);
-      }
-    }
-    inv[q] = rsqrtf(wave_sum(qq) / D + eps);
-  }
+      if (lane + 64 * j < nc) s[q] += (v[q][j].x + v[q][j].y) + (v[q][j].z + v[q][j].w);
 #pragma unroll
   for (int q = 0; q < RPW; q++) {
     const int row = row0 + q;
     if (row >= rows) break;
+    const float mean = wave_sum(s[q]) / D;
+    float qq = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const int c = lane + 64 * j;
+      if (c < nc) {
+        const float a = v[q][j].x - mean, bb = v[q][j].y - mean, cc = v[q][j].z - mean, d = v[q][j].w - mean;
+        qq += (a * a + bb * bb) + (cc * cc + d * d);
+      }
+    }
+    const float inv = rsqrtf(wave_sum(qq) / D + eps);
     const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
       if (c < nc) {
-        const float4 ww4 = ww[j];
-        float4 o = make_float4((v[q][j].x - mean[q]) * inv[q] * ww4.x, (v[q][j].y - mean[q]) * inv[q] * ww4.y,
-                               (v[q][j].z - mean[q]) * inv[q] * ww4.z, (v[q][j].w - mean[q]) * inv[q] * ww4.w);
-        if (b) { o.x += bb[j].x; o.y += bb[j].y; o.z += bb[j].z; o.w += bb[j].w; }
+        const float4 ww = reinterpret_cast<const float4*>(w)[c];
+        float4 o = make_float4((v[q][j].x - mean) * inv * ww.x, (v[q][j].y - mean) * inv * ww.y,
+                               (v[q][j].z - mean) * inv * ww.z, (v[q][j].w - mean) * inv * ww.w);
+        if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
         if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
         if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
         if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
@@ -109,20 +95,23 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
   }
 }
 
-// One row per wave: a 1024-wide row is 4 KiB of fp32, and with one row per wave every workgroup
-// of the launch is resident at once (about 2400 workgroups for 9.5k rows), which measured faster
-// than two or four rows per wave (fewer, longer waves).
+// Two rows per wave for rows up to 1024 wide (about 2400 waves for 9.6k rows, 60 VGPRs: eight
+// waves per SIMD, so all of them are resident at once).  In the pass a LayerNorm starts cold after
+// a GEMM; one row per wave (twice the wave launches) or weights held in registers across the
+// reductions (125 VGPRs, half the occupancy) both measured slower there.
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
                       const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st) {
   if (D % 4 || D > kLnMaxChunks * 256) { fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D); exit(1); }
   if (rows <= 0) return;
-  if (D <= 1024)
-    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, 4>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps,
-                       w, b, addtab, qt, seq, y32, yT);
-  else
-    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows,
-                       D, eps, w, b, addtab, qt, seq, y32, yT);
+  if (D <= 1024) {
+    constexpr int RPW = 2;
+    hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x, gather,
+                       rows, D, eps, w, b, addtab, qt, seq, y32, yT);
+  } else {
+    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
+                       addtab, qt, seq, y32, yT);
+  }
 }
 
 template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
