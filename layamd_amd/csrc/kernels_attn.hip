@@ -255,7 +255,7 @@ __device__ __forceinline__ u32x4_t attn_rsrc(const void* p, uint32_t bytes) {
   return r;
 }
 
-__global__ __launch_bounds__(128) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
                                                         int ldqk, int kv_rows, const bf16_t* __restrict__ Vt, int ldv,
                                                         int vt_rows, bf16_t* __restrict__ O, int ldo,
                                                         const AttnTile* __restrict__ tiles, const int* __restrict__ soff,
