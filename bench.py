@@ -134,9 +134,13 @@ def main():
     mdir = ck.cached_checkpoint(cfg.name)
     print("[bench] checkpoint %s ready in %.1fs" % (mdir, time.time() - t0), file=sys.stderr, flush=True)
     max_tokens = max(16384, int(batch.tokens) + 1024)
-    eng = le.Engine(None, mdir, precision=precision, env={"LAYA_MAX_TOKENS": max_tokens,
-                                                         "LAYA_GRAPHS": 0 if a.pmc_probe else 1,
-                                                         "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None})
+    env = {"LAYA_MAX_TOKENS": max_tokens, "LAYA_GRAPHS": 0 if a.pmc_probe else 1, "LAYA_DUMP_DIR": None,
+           "LAYA_PROFILE": None}
+    if a.pmc_probe:
+        # counter runs serialize every dispatch, so tile timing is meaningless there: pin the plan the
+        # tuner picks for the dominant stage at this workload (256x256 over 9216 rows, 128x128 after)
+        env.update({"LAYA_GEMM_CFG": 0, "LAYA_GEMM_SPLIT": "9216,3"})
+    eng = le.Engine(None, mdir, precision=precision, env=env)
     flat = batch.flat()
     if a.pmc_probe:
         src = torch.ones(PMC_COPY_BYTES, dtype=torch.uint8, device="cuda")

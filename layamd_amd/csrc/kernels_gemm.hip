@@ -860,12 +860,22 @@ static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80
 // launch, gemm_config() at run time
 static std::atomic<int> g_gemm_cfg{-2};
 
+// row split applied with the pinned configuration (0: none)
+static std::atomic<int> g_split_rows{0}, g_cfg_tail{-1};
+
 int gemm_pinned() {
   int v = g_gemm_cfg.load(std::memory_order_relaxed);
   if (v == -2) {
     const char* e = getenv("LAYA_GEMM_CFG");
     v = e ? atoi(e) : -1;
     if (v < -1 || v >= kGemmConfigs) v = -1;
+    // LAYA_GEMM_SPLIT=rows,cfg: with a pinned configuration, rows [rows, M) in a second launch
+    const char* sp = getenv("LAYA_GEMM_SPLIT");
+    int rows = 0, tail = -1;
+    if (v >= 0 && sp && sscanf(sp, "%d,%d", &rows, &tail) == 2 && rows > 0 && tail >= 0 && tail < kGemmConfigs) {
+      g_split_rows.store(rows, std::memory_order_relaxed);
+      g_cfg_tail.store(tail, std::memory_order_relaxed);
+    }
     g_gemm_cfg.store(v, std::memory_order_relaxed);
   }
   return v;
@@ -876,9 +886,6 @@ int gemm_config(int cfg) {
   g_gemm_cfg.store(cfg, std::memory_order_relaxed);
   return prev;
 }
-
-// row split applied with the pinned configuration (0: none)
-static std::atomic<int> g_split_rows{0}, g_cfg_tail{-1};
 
 void gemm_pin_split(int split_rows, int cfg_tail) {
   g_split_rows.store(split_rows, std::memory_order_relaxed);
