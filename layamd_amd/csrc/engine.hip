@@ -118,10 +118,13 @@ struct Engine : EngineIface {
   float *x = nullptr, *xg = nullptr, *d_logits = nullptr, *d_act = nullptr, *d_act_hidden = nullptr;
   T *xn, *q, *k, *vt, *ao, *mg, *ff, *aog, *xng, *sh;
 
-  // per-pass index arrays: device + pinned host mirrors at fixed addresses (graph replay)
+  // per-pass index arrays: one device block and its pinned host mirror, laid out per pass shape
+  // (so a captured graph's addresses hold for every replay of that shape) and uploaded by one copy
   int *d_ids, *d_pos, *d_seq, *d_soff, *d_vlen, *d_qt, *d_nm, *d_moff, *d_gq, *d_grow;
   int *h_ids, *h_pos, *h_seq, *h_soff, *h_vlen, *h_qt, *h_nm, *h_moff, *h_gq, *h_grow;
   AttnTile *d_tiles, *d_gtiles, *h_tiles, *h_gtiles;
+  char *d_blob = nullptr, *h_blob = nullptr;
+  size_t blob_cap = 0;
   float *h_logits, *h_act;
 
   struct Shape {
@@ -317,14 +320,14 @@ struct Engine : EngineIface {
     d_act_hidden = dalloc<float>((size_t)lim.max_seqs * 256);
     h_logits = halloc<float>((size_t)RG);
     h_act = halloc<float>((size_t)lim.max_seqs * cfg.n_act);
-    auto pair = [&](int** d, int** h, size_t n) { *d = dalloc<int>(n); *h = halloc<int>(n); };
-    pair(&d_ids, &h_ids, MT); pair(&d_pos, &h_pos, MT); pair(&d_seq, &h_seq, MT);
-    pair(&d_soff, &h_soff, lim.max_seqs + 1); pair(&d_vlen, &h_vlen, lim.max_seqs);
-    pair(&d_qt, &h_qt, lim.max_seqs);
-    pair(&d_nm, &h_nm, lim.max_seqs); pair(&d_moff, &h_moff, lim.max_seqs);
-    pair(&d_gq, &h_gq, RG); pair(&d_grow, &h_grow, RG);
-    d_tiles = dalloc<AttnTile>(caps.tiles); h_tiles = halloc<AttnTile>(caps.tiles);
-    d_gtiles = dalloc<AttnTile>(caps.gtiles); h_gtiles = halloc<AttnTile>(caps.gtiles);
+    {
+      const Shape cap{(int)MT, lim.max_seqs, (int)RG, (int)RG, (int)caps.tiles, (int)caps.gtiles};
+      blob_cap = blob_layout(cap).total;
+      d_blob = dalloc<char>(blob_cap);
+      h_blob = halloc<char>(blob_cap);
+      memset(h_blob, 0, blob_cap);
+      bind(cap);
+    }
 
     LAYA_HIP(hipStreamCreate(&stream));
     {
@@ -343,6 +346,30 @@ struct Engine : EngineIface {
   }
 
   // ------------------------------------------------------------ one pass
+  // byte offsets of the index arrays of a pass shape in the blocks (256-byte aligned)
+  struct BlobLayout { size_t ids, pos, seq, soff, vlen, qt, nm, moff, gq, grow, tiles, gtiles, total; };
+  static BlobLayout blob_layout(const Shape& s) {
+    BlobLayout L;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { const size_t r = o; o += (bytes + 255) & ~(size_t)255; return r; };
+    L.ids = take((size_t)s.rows * 4); L.pos = take((size_t)s.rows * 4); L.seq = take((size_t)s.rows * 4);
+    L.soff = take((size_t)(s.B + 1) * 4); L.vlen = take((size_t)s.B * 4); L.qt = take((size_t)s.B * 4);
+    L.nm = take((size_t)s.B * 4); L.moff = take((size_t)s.B * 4);
+    L.gq = take((size_t)s.R * 4); L.grow = take((size_t)s.R * 4);
+    L.tiles = take((size_t)s.nt * sizeof(AttnTile)); L.gtiles = take((size_t)s.ngt * sizeof(AttnTile));
+    L.total = o;
+    return L;
+  }
+  void bind(const Shape& s) {
+    const BlobLayout L = blob_layout(s);
+    auto at = [&](size_t off, int** d, int** h) { *d = (int*)(d_blob + off); *h = (int*)(h_blob + off); };
+    at(L.ids, &d_ids, &h_ids); at(L.pos, &d_pos, &h_pos); at(L.seq, &d_seq, &h_seq);
+    at(L.soff, &d_soff, &h_soff); at(L.vlen, &d_vlen, &h_vlen); at(L.qt, &d_qt, &h_qt);
+    at(L.nm, &d_nm, &h_nm); at(L.moff, &d_moff, &h_moff); at(L.gq, &d_gq, &h_gq); at(L.grow, &d_grow, &h_grow);
+    d_tiles = (AttnTile*)(d_blob + L.tiles); h_tiles = (AttnTile*)(h_blob + L.tiles);
+    d_gtiles = (AttnTile*)(d_blob + L.gtiles); h_gtiles = (AttnTile*)(h_blob + L.gtiles);
+  }
+
   void stage_inputs(const PassPlan& p) {
     memcpy(h_ids, p.ids.data(), p.T * 4); memcpy(h_pos, p.pos.data(), p.T * 4);
     memcpy(h_seq, p.seq.data(), p.T * 4);
@@ -471,10 +498,9 @@ struct Engine : EngineIface {
   // the scorer share the encoder's and head's (N, K) shapes at other M)
   void tune_all() override {
     if (tune_on && sizeof(T) == 2 && gemm_pinned() < 0) {
-      // the listing run uploads these host mirrors: position 0 keeps the RoPE table reads in range
-      for (int64_t i = 0; i < MT; i++) { h_pos[i] = 0; h_seq[i] = 0; h_ids[i] = 0; }
-      for (int64_t i = 0; i < RG; i++) { h_gq[i] = 0; h_grow[i] = 0; }
-      h_soff[0] = 0; h_soff[1] = 0; h_vlen[0] = 0; h_qt[0] = 0; h_nm[0] = 0; h_moff[0] = 0;
+      // the listing run uploads the host block: all zeros (position 0) keeps the RoPE table reads
+      // in range whatever the layout
+      memset(h_blob, 0, blob_cap);
       for (int mb = 64; mb <= MT; mb = m_bucket(mb + 1)) {
         const int r = (int)std::min<int64_t>(mb, RG);
         tune_pass(Shape{mb, 1, r - 1, r, 0, 0});
@@ -489,11 +515,8 @@ struct Engine : EngineIface {
     const int T_ = s.rows, B = s.B, KT = s.KT, R = s.R;
     hipStream_t st = stream;
     auto h2d = [&](void* d, const void* h, size_t n) { LAYA_HIP(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st)); };
-    h2d(d_ids, h_ids, T_ * 4); h2d(d_pos, h_pos, T_ * 4); h2d(d_seq, h_seq, T_ * 4);
-    h2d(d_soff, h_soff, (B + 1) * 4); h2d(d_vlen, h_vlen, B * 4);
-    h2d(d_qt, h_qt, B * 4); h2d(d_nm, h_nm, B * 4); h2d(d_moff, h_moff, B * 4);
-    h2d(d_gq, h_gq, R * 4); h2d(d_grow, h_grow, R * 4);
-    h2d(d_tiles, h_tiles, s.nt * sizeof(AttnTile)); h2d(d_gtiles, h_gtiles, s.ngt * sizeof(AttnTile));
+    bind(s);
+    h2d(d_blob, h_blob, blob_layout(s).total);
 
     // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
 #define STAGE(name, ...) do { if (!collecting) { prof.start(st); __VA_ARGS__; prof.stop(name, st); } } while (0)
@@ -637,8 +660,9 @@ struct Engine : EngineIface {
     std::vector<int64_t> moff(B + 1, 0);
     for (int b = 0; b < B; b++) moff[b + 1] = moff[b] + nmark[b];
     for (const PassPlan& p : passes) {
-      stage_inputs(p);
       Shape s{p.T, p.B, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size()};
+      bind(s);
+      stage_inputs(p);
       execute(s);
       for (int i = 0; i < p.B; i++) {
         const int b = p.first + i;

@@ -182,41 +182,73 @@ template void launch_row_dot<bf16_t>(const bf16_t*, int, const float*, const flo
 // p = softmax(logits over the question's markers); k = max(nmark, 2); features [top1,
 // top1 - top2, -sum p log(max(p, 1e-9)) / ln k, k / 255]; hidden = GELU(W0 [cls, features] + b0)
 // with W0 [256][D + 4]; out = W2 hidden + b2.
-// k_act_hidden: grid (B, 16); each workgroup recomputes the question's 4 features (<= 255 logits)
-// and produces 16 hidden units, one wave per 4 units with lanes striding over D + 4.
+// k_act_hidden: grid (B, 16); each wave produces 4 hidden units.  The W0 . cls partial sums are
+// issued first (their loads do not depend on the features); then every wave computes the
+// question's 4 features itself from its <= 255 logits (lanes over markers, wave reductions), so no
+// barrier is needed.  top2 is the second largest probability counted with multiplicity (top1 again
+// when the maximum occurs twice), 0 when there is none.
 __global__ __launch_bounds__(256) void k_act_hidden(const float* __restrict__ cls, int D, const float* __restrict__ logits,
                                                     const int* __restrict__ moff, const int* __restrict__ nmark,
                                                     const float* __restrict__ W0, const float* __restrict__ B0,
                                                     float* __restrict__ hidden) {
-  __shared__ float feat[4];
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  if (t == 0) {
-    const float* z = logits + moff[b];
-    const int K = nmark[b];
-    float mx = -INFINITY;
-    for (int i = 0; i < K; i++) mx = fmaxf(mx, z[i]);
-    float s = 0.f;
-    for (int i = 0; i < K; i++) s += expf(z[i] - mx);
-    float t1 = 0.f, t2 = 0.f, ent = 0.f;
-    for (int i = 0; i < K; i++) {
-      const float p = expf(z[i] - mx) / s;
-      ent -= p * logf(fmaxf(p, 1e-9f));
-      if (p > t1) { t2 = t1; t1 = p; } else if (p > t2) t2 = p;
-    }
-    const float k = (float)(K < 2 ? 2 : K);
-    feat[0] = t1; feat[1] = t1 - t2; feat[2] = ent / logf(k); feat[3] = k / 255.f;
-  }
-  __syncthreads();
   const float* c = cls + (size_t)b * D;
+  const int j0 = blockIdx.y * 16 + wv * 4;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = lane; i < D; i += 64) {
+    const float ci = c[i];
+#pragma unroll
+    for (int u = 0; u < 4; u++) a[u] += W0[(size_t)(j0 + u) * (D + 4) + i] * ci;
+  }
+
+  const float* z = logits + moff[b];
+  const int K = nmark[b];
+  float zl[4], mx = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int i = lane + 64 * q;
+    zl[q] = i < K ? z[i] : -INFINITY;
+    mx = fmaxf(mx, zl[q]);
+  }
+  mx = wave_max(mx);
+  float e[4], se = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    e[q] = lane + 64 * q < K ? expf(zl[q] - mx) : 0.f;
+    se += e[q];
+  }
+  se = wave_sum(se);
+  float p[4], ent = 0.f, t1 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    p[q] = e[q] / se;
+    if (lane + 64 * q < K) {
+      ent -= p[q] * logf(fmaxf(p[q], 1e-9f));
+      t1 = fmaxf(t1, p[q]);
+    }
+  }
+  ent = wave_sum(ent);
+  t1 = wave_max(t1);
+  float n1 = 0.f, t2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (lane + 64 * q < K) {
+      if (p[q] == t1) n1 += 1.f;
+      else t2 = fmaxf(t2, p[q]);
+    }
+  }
+  n1 = wave_sum(n1);
+  t2 = n1 >= 2.f ? t1 : wave_max(t2);
+  const float kf = (float)(K < 2 ? 2 : K);
+  const float feat = lane == 0 ? t1 : lane == 1 ? t1 - t2 : lane == 2 ? ent / logf(kf) : kf / 255.f;
+
 #pragma unroll
   for (int u = 0; u < 4; u++) {
-    const int j = blockIdx.y * 16 + wv * 4 + u;
-    const float* wr = W0 + (size_t)j * (D + 4);
-    float a = 0.f;
-    for (int i = lane; i < D; i += 64) a += wr[i] * c[i];
-    if (lane < 4) a += wr[D + lane] * feat[lane];
-    a = wave_sum(a);
-    if (lane == 0) hidden[(size_t)b * 256 + j] = gelu_erf(a + B0[j]);
+    const int j = j0 + u;
+    float v = a[u];
+    if (lane < 4) v += W0[(size_t)j * (D + 4) + D + lane] * feat;
+    v = wave_sum(v);
+    if (lane == 0) hidden[(size_t)b * 256 + j] = gelu_erf(v + B0[j]);
   }
 }
 
