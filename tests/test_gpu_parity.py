@@ -262,19 +262,18 @@ def test_multi_pass_split():
 
 
 # ---------------------------------------------------------------- ModernBERT-large
-def test_large_fp32_c1_golden():
-    """ModernBERT-large + head, fp32, batch 1 x 128 against the reference model's own output."""
-    g = np.load(os.path.join(GOLDEN, "large", "golden.npz"))
-    man = json.load(open(os.path.join(GOLDEN, "large", "manifest.json")))
-    cfg = ck.PRESETS["large"]
-    b = wl.c1(0)
+def _full_size_fp32_golden(tag, b):
+    """fp32 engine against a full-size golden set: sampled rows of every layer, probabilities, act."""
+    g = np.load(os.path.join(GOLDEN, tag, "golden.npz"))
+    man = json.load(open(os.path.join(GOLDEN, tag, "manifest.json")))
+    cfg = ck.PRESETS[man["model"]["preset"]]
     lens, ids, nm, mk, qt = b.flat()
-    assert np.array_equal(ids, g["input_ids"][0])
+    assert np.array_equal(ids, g["input_ids"][0][:lens[0]])
     with tempfile.TemporaryDirectory() as dd:
-        e = engine("large", "fp32", LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0)
+        e = engine(tag, "fp32", LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0)
         lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
         rows = g["sample_rows"]
-        W_type = ck.read_safetensors(os.path.join(checkpoint_dir("large"), "model.safetensors"))["type_emb.weight"]
+        W_type = ck.read_safetensors(os.path.join(checkpoint_dir(tag), "model.safetensors"))["type_emb.weight"]
         worst = 0.0
         for name in man["layers"]:
             fname = {"final_norm": "final"}.get(name, name)
@@ -287,10 +286,22 @@ def test_large_fp32_c1_golden():
             err = np.abs(got - ref).max()
             worst = max(worst, err)
             assert err < FP32_HIDDEN, (name, err)
-        print("large fp32 worst per-layer max-abs %.3g" % worst)
+        print("%s fp32 worst per-layer max-abs %.3g" % (tag, worst))
     gl = g["logits"][0, :nm[0]]
     assert prob_delta(lo, gl, nm) < FP32_PROB
     assert (np.abs(ac - g["act_logits"]) / np.maximum(1, np.abs(g["act_logits"]))).max() < FP32_ACT
+
+
+def test_large_fp32_c1_golden():
+    """ModernBERT-large + head, fp32, batch 1 x 128 against the reference model's own output."""
+    _full_size_fp32_golden("large", wl.c1(0))
+
+
+def test_base_fp32_golden():
+    """mmBERT-base shape (22 layers, D 768, 12 heads, I 1152, V 256000) + head, fp32, batch 1 x 200,
+    against the reference model's own output."""
+    b = wl.make_batch(ck.PRESETS["base"], [200], [4], seed=7, dtype="fp32", name="base-b1s200")
+    _full_size_fp32_golden("base", b)
 
 
 def test_large_bf16_c1_drift():
@@ -350,6 +361,46 @@ def test_gemm_tuning_keeps_outputs():
     assert np.isfinite(lo0).all() and np.isfinite(ac0).all()
     for lo, ac in ((lo1, ac1), (lo2, ac2)):
         assert np.array_equal(lo, lo0) and np.array_equal(ac, ac0)
+
+
+def test_base_bf16_c4_sample_vs_oracle():
+    """Two questions of the mmBERT-base-shaped b16 x s1024 batch (lengths 972 and 966) in bf16
+    against the fp32 CPU oracle."""
+    import torch
+    from oracle import model as om
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    cfg, W = ck.load_checkpoint(checkpoint_dir("base"))
+    b = wl.c4(0).subset([11, 15])
+    lo, ac = engine("base", "bf16").forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["base"], b)
+    d = prob_delta(lo, ref_lo, b.nmark)
+    print("c4 sample bf16 dprob %.5f lens %s" % (d, list(b.lens)))
+    assert d < BF16_PROB
+
+
+def test_large1024_bf16_c5_sample_vs_oracle():
+    """Three sequences of the ModernBERT-large (1024 context) b64 x s1024 batch with 25-29 markers
+    each (eight questions of 2-5 options per sequence) in bf16 against the fp32 CPU oracle; the
+    whole 64-sequence batch (18k tokens, one pass) must give the same logits for them."""
+    import torch
+    from oracle import model as om
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    d = ck.cached_checkpoint("large1024")
+    cfg, W = ck.load_checkpoint(d)
+    full = wl.c5(0)
+    pick = [50, 17, 24]
+    b = full.subset(pick)
+    e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=32768))
+    lo, ac = e.forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["large1024"], b)
+    dp = prob_delta(lo, ref_lo, b.nmark)
+    print("c5 sample bf16 dprob %.5f lens %s nmark %s" % (dp, list(b.lens), list(b.nmark)))
+    assert dp < BF16_PROB
+    flo, fac = e.forward_flat(*full.flat())
+    moff = np.concatenate([[0], np.cumsum(full.nmark)])
+    got = np.concatenate([flo[moff[i]:moff[i + 1]] for i in pick])
+    assert np.array_equal(got, lo)
+    assert np.array_equal(fac.reshape(64, -1)[pick], ac.reshape(len(pick), -1))
 
 
 def test_large_bf16_c3_sample_vs_oracle():
