@@ -1,18 +1,23 @@
-// MFMA GEMM for gfx950: C[M,N] = A[M,K] . W[N,K]^T with fused epilogues.
+// MFMA GEMMs for gfx950: C[M,N] = A[M,K] . W[N,K]^T with fused epilogues.
 //
 // Both operands are K-contiguous (activations [rows, K], weights in their checkpoint [out, in]
-// layout), which is the layout the MFMA operand registers want: a lane of
-// v_mfma_f32_16x16x32_bf16 holds 8 consecutive K values of one row of A and one column of B, so
-// every fragment is one 16-byte LDS read and no weight is ever transposed.  The fp32 path uses
-// v_mfma_f32_16x16x4_f32 on the same tiles (a 16-byte chunk = 4 K values = 4 MFMAs).
+// layout), which is the layout the MFMA operand registers want: a lane holds 8 consecutive K values
+// of one row of each operand, so every fragment is one 16-byte LDS read and no weight is ever
+// transposed.  Two kernels:
 //
-// Tiling: a 256-thread workgroup (4 wave64s in a WM x WN grid) computes a BM x BN tile; K
-// advances in 128-byte slices (64 bf16 / 32 fp32) through double-buffered LDS with an XOR
-// swizzle of the 16-byte chunks (chunk ^ (row & 7)) so a fragment read by 16 lanes covers all
-// banks.  The next slice is fetched into registers while the current one feeds the MFMAs.
-// Workgroup ids are remapped so each of the 8 XCDs (own L2) walks a contiguous run of tiles.
+//   k_gemm_xl  bf16, the engine's path.  256-thread workgroups, tiles from 128x128 to 256x256 on
+//              v_mfma_f32_32x32x16_bf16; K advances in 32-deep slices through five LDS stages
+//              filled four slices ahead by LDS DMA (buffer_load ... lds); the product is computed
+//              transposed so each lane holds four consecutive output columns; the epilogue is
+//              staged through LDS and leaves as full-line 16-byte stores.  The engine picks the
+//              tile shape (and an optional row split over two launches) per GEMM by timing.
+//   k_gemm     fp32 operands, and bf16 shapes the tiled kernel cannot take (unaligned N or
+//              strides).  128x128 tiles, K in 128-byte slices through double-buffered LDS with
+//              register prefetch, v_mfma_f32_16x16x4_f32 / v_mfma_f32_16x16x32_bf16.
 //
-// Epilogues (accumulator element i of lane l in a 16x16 block is row 4*(l/16)+i, col l%16):
+// Both remap workgroup ids so each of the 8 XCDs (own L2) walks a contiguous run of tiles.
+//
+// Epilogues:
 //   EPI_STORE  C = act(acc + bias)                        (storage type)
 //   EPI_RESID  X += acc + bias                            (fp32 residual stream)
 //   EPI_QKV    q,k (RoPE when tables are given) -> Q, K [rows][H*HD]; v -> V^T [H*HD][ldv] at
@@ -141,6 +146,7 @@ __global__ __launch_bounds__(256) void k_gemm(const GemmArgs a) {
   }
 
   // ---------------- epilogue ----------------
+  // accumulator element i of lane l in a 16x16 block is row 4 (l / 16) + i, column l % 16
   const int rbase = m0 + wm * WTM + 4 * g, cbase = n0 + wn * WTN;
   if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
 #pragma unroll

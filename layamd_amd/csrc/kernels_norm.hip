@@ -1,8 +1,8 @@
 // LayerNorm family, gathers, and the decision head's small kernels for gfx950.
 //
-// LayerNorm is HBM-bound: one wave64 owns one row, keeps it in registers (D/256 float4 per
-// lane), reduces mean and variance with wave shuffles (no LDS, no barriers), and writes the
-// normalised row in one pass.  Four rows per 256-thread workgroup.
+// LayerNorm is HBM-bound: one wave64 owns two rows (one above 1024 columns), keeps them in
+// registers (D/256 float4 per lane and row), reduces mean and variance with wave shuffles (no
+// LDS, no barriers), and writes the normalised rows in one pass.  Four waves per workgroup.
 #include "kernels.h"
 
 namespace laya {
