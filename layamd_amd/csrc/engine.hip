@@ -5,14 +5,16 @@
 //
 //   embeddings -> LN                                   k_layernorm (gather by token id)
 //   per encoder layer:
-//     QKV GEMM + RoPE + V^T write                      k_gemm<EPI_QKV>
-//     attention (global | sliding +-64)                k_attention
-//     out-proj GEMM, x += (fp32 residual)               k_gemm<EPI_RESID>
+//     QKV GEMM + RoPE + V^T write                      k_gemm_xl<EPI_QKV>
+//     attention (global | sliding +-64)                k_attention_bf16
+//     out-proj GEMM, x += (fp32 residual)               k_gemm_xl<EPI_RESID>
 //     LN -> xn                                         k_layernorm
-//     Wi GEMM + GeGLU                                  k_gemm<EPI_GEGLU>
-//     Wo GEMM, x +=                                    k_gemm<EPI_RESID>
+//     Wi GEMM + GeGLU                                  k_gemm_xl<EPI_GEGLU>
+//     Wo GEMM, x +=                                    k_gemm_xl<EPI_RESID>
 //     LN -> xn (next attn_norm) | final LN + type embedding into x
 //   head layer 0 (all rows), head layer 1 on the gathered marker + CLS rows, scorer, act head.
+// (bf16 names; the fp32 engine runs k_gemm and k_attention<float>.)  The GEMM tile shapes of a
+// pass are timed before its first run (tune_pass) and the pass is then captured in a HIP graph.
 //
 // Semantics follow the reference's Engine::run / forward_batch (src/engine.hip:396-539) and the
 // upstream model it serves (ref/rl_common.py:100-124); the kernels, data layout and fusion are

@@ -1,4 +1,6 @@
 // Attention over packed variable-length sequences for gfx950 (wave64 MFMA, fp32 online softmax).
+// Two kernels: k_attention_bf16 (the bf16 engine's, described above it) and k_attention<T>, the
+// fp32 engine's, described here.
 //
 // One 256-thread workgroup owns one query tile (<= 64 queries of one sequence) of one head;
 // each wave64 owns 16 queries.  Keys advance in blocks of 64: the workgroup stages the block's
