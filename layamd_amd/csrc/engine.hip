@@ -317,6 +317,7 @@ struct Engine : EngineIface {
     ff = dalloc<T>((size_t)std::max(MT, RG) * FF);
     xg = dalloc<float>((size_t)RG * D);
     aog = dalloc<T>((size_t)RG * D); xng = dalloc<T>((size_t)RG * D); sh = dalloc<T>((size_t)RG * D);
+    if (sizeof(T) == 2) sk_ws = dalloc<float>(kSplitKBytes / sizeof(float));
     d_logits = dalloc<float>((size_t)RG);
     d_act = dalloc<float>((size_t)lim.max_seqs * cfg.n_act);
     d_act_hidden = dalloc<float>((size_t)lim.max_seqs * 256);
@@ -391,6 +392,18 @@ struct Engine : EngineIface {
     std::string fn = std::string(dump_dir) + "/" + name + ".bin";
     FILE* f = fopen(fn.c_str(), "wb");
     if (f) { fwrite(buf.data(), 4, buf.size(), f); fclose(f); }
+  }
+
+  // Split-K for the GEMMs on the gathered rows and the scorer (a few hundred rows, so without it
+  // a handful of tiles would each walk the whole K).  The factor depends only on K, never on how
+  // many rows a batch gathered, so a row's result is the same in every batch.
+  static constexpr size_t kSplitKBytes = (size_t)64 << 20;
+  float* sk_ws = nullptr;
+  void splitk(GemmArgs& g) const {
+    if (sizeof(T) != 2 || !sk_ws) return;
+    g.ksplit = g.K >= 2048 ? 16 : 8;
+    g.ws = sk_ws;
+    g.ws_bytes = kSplitKBytes;
   }
 
   GemmArgs gemm_args(const T* A, int lda, const T* W, int M, int N, int K, const float* bias) {
@@ -490,7 +503,7 @@ struct Engine : EngineIface {
     collecting = nullptr;
     for (auto& eg : list) {
       const TuneKey key = tune_key(eg.first, eg.second);
-      if (!tuned.count(key)) tuned[key] = tune_gemm(eg.first, eg.second);
+      if (eg.second.ksplit <= 1 && !tuned.count(key)) tuned[key] = tune_gemm(eg.first, eg.second);
     }
     LAYA_HIP(hipStreamSynchronize(stream));
     tuned_shapes.insert(s);
@@ -597,13 +610,13 @@ struct Engine : EngineIface {
         STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
                                                         d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
-        { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D;
+        { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D; splitk(g);
           GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
         STAGE("head:ln", launch_layernorm<float, T>(xg, nullptr, R, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
                                                     nullptr, xng, st));
         { GemmArgs g = gemm_args(xng, D, hl.l1W, R, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
           GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
-        { GemmArgs g = gemm_args(ff, FF, hl.l2W, R, D, FF, hl.l2B); g.X = xg; g.ldx = D;
+        { GemmArgs g = gemm_args(ff, FF, hl.l2W, R, D, FF, hl.l2B); g.X = xg; g.ldx = D; splitk(g);
           GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d_gathered", L); dump(nm, xg, R); }
       }
@@ -611,7 +624,7 @@ struct Engine : EngineIface {
     // scorer on the KT marker rows: LN(+bias) -> Linear + GELU -> Linear(D -> 1)
     STAGE("scorer:ln", launch_layernorm<float, T>(xg, nullptr, KT, D, eps, sc0w, sc0b, nullptr, nullptr, nullptr,
                                                   nullptr, xng, st));
-    { GemmArgs g = gemm_args(xng, D, sc1W, KT, D, D, sc1b); g.C = sh; g.ldc = D; g.act = ACT_GELU;
+    { GemmArgs g = gemm_args(xng, D, sc1W, KT, D, D, sc1b); g.C = sh; g.ldc = D; g.act = ACT_GELU; splitk(g);
       GSTAGE("scorer:gemm_gelu", gemm(EPI_STORE, g, st)); }
     STAGE("scorer:dot", launch_row_dot<T>(sh, D, sc3w, sc3b, d_logits, KT, D, st));
     STAGE("act_head", launch_act_head(xg + (size_t)KT * D, D, d_logits, d_moff, d_nm, ah0W, ah0b, ah2W, ah2b,
@@ -749,6 +762,9 @@ int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, lo
   return 0;
 }
 int laya_ext_replay(void* h, int iters, float* ms) { return E(h)->replay(iters, ms); }
+static float* g_ext_ws = nullptr;          // split-K workspace of laya_ext_gemm (caller's memory)
+static size_t g_ext_ws_bytes = 0;
+
 int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
                   int K, void* stream, int iters, float* ms) {
   using namespace laya;
@@ -759,6 +775,9 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
   const char* why = "";
   if (!gemm_shape_ok(epi == 0 ? EPI_STORE : EPI_RESID, g, dtype == 0 ? 4 : 2, &why)) return -1;
   hipStream_t st = (hipStream_t)stream;
+  // a pinned split-K factor runs in the caller's workspace (laya_ext_gemm_ksplit)
+  g.ws = g_ext_ws;
+  g.ws_bytes = g_ext_ws_bytes;
   hipEvent_t a, b;
   if (ms) { LAYA_HIP(hipEventCreate(&a)); LAYA_HIP(hipEventCreate(&b)); LAYA_HIP(hipEventRecord(a, st)); }
   for (int i = 0; i < iters; i++) {
@@ -775,6 +794,12 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
   return 0;
 }
 const char* laya_ext_precision(void* h) { return E(h)->precision(); }
+int laya_ext_gemm_ksplit(int ks, void* ws, size_t ws_bytes) {
+  if (ks < 0 || ks > 64 || (ks > 1 && (!ws || ws_bytes == 0))) return -2;
+  g_ext_ws = static_cast<float*>(ws);
+  g_ext_ws_bytes = ws_bytes;
+  return laya::gemm_pin_ksplit(ks);
+}
 int laya_ext_gemm_config(int cfg) {
   if (cfg < -1 || cfg >= laya::kGemmConfigs) return -2;
   return laya::gemm_config(cfg);

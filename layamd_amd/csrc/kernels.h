@@ -23,7 +23,8 @@ template <typename T>
 void launch_fill_pattern(T* p, size_t n, uint32_t seed, hipStream_t st);
 
 // ---- MFMA GEMM: C = A[M,K] . W[N,K]^T with a fused epilogue ----
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GEGLU = 3 };
+// EPI_PARTIAL is internal to split-K: fp32 partial products of one K chunk, no bias
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_GEGLU = 3, EPI_PARTIAL = 4 };
 enum GemmAct { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
 
 struct GemmArgs {
@@ -44,6 +45,13 @@ struct GemmArgs {
   // rows [split_rows, M) run as a second launch with configuration cfg_tail (0: one launch); the
   // first launch then covers whole rounds of large tiles and the second the few rows left over
   int split_rows = 0, cfg_tail = -1;
+  // split-K (bf16 EPI_STORE / EPI_RESID): K in ksplit equal chunks whose fp32 partial products go to
+  // the workspace ws (ws_bytes; rows are processed in chunks that fit it) and are summed in chunk
+  // order, then bias, activation or the residual add.  The result of a row depends on ksplit, not
+  // on M, so a call site that always passes the same ksplit stays independent of the batch.
+  int ksplit = 1;
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
 };
 
 template <typename T>
@@ -56,6 +64,9 @@ int gemm_pinned();                               // the pinned configuration, or
 // row split used together with the pinned configuration: rows [split_rows, M) run as a second
 // launch with cfg_tail (split_rows 0: none)
 void gemm_pin_split(int split_rows, int cfg_tail);
+// split-K factor applied to later bf16 EPI_STORE / EPI_RESID launches that name none (<= 1: none);
+// returns the previous one
+int gemm_pin_ksplit(int ks);
 constexpr int kGemmConfigs = 5;
 // whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
 // shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)

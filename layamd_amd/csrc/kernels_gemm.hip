@@ -518,8 +518,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
   const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
+  // split-K partials: workgroup split * tiles + t computes tile t over K chunk `split` (a.K deep)
+  int bid = blockIdx.x, split = 0;
+  if constexpr (EPI == EPI_PARTIAL) {
+    split = bid / (tilesM * tilesN);
+    bid -= split * tilesM * tilesN;
+  }
   int tm, tn;
-  tile_coords(blockIdx.x, tilesM, tilesN, tm, tn);
+  tile_coords(bid, tilesM, tilesN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int D = a.H * a.HD;
   // all tiles use the transposed product except the V columns of the QKV projection, which are
@@ -539,8 +545,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   }
 
   XlDma<PA, PB> dm;
-  dm.rA = make_rsrc(a.A, (uint32_t)((size_t)a.M * a.lda * sizeof(T)));
-  dm.rB = make_rsrc(a.W, (uint32_t)((size_t)a.N * a.ldw * sizeof(T)));
+  const size_t k0 = (size_t)split * a.K;                 // first K column of this workgroup
+  dm.rA = make_rsrc(reinterpret_cast<const T*>(a.A) + k0, (uint32_t)(((size_t)a.M * a.lda - k0) * sizeof(T)));
+  dm.rB = make_rsrc(reinterpret_cast<const T*>(a.W) + k0, (uint32_t)(((size_t)a.N * a.ldw - k0) * sizeof(T)));
   dm.rNone = make_rsrc(a.A, 0u);           // zero length: every offset out of range
   const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
 #pragma unroll
@@ -642,8 +649,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     if constexpr (HB) return v + b;
     else return v;
   };
-  if constexpr (EPI == EPI_RESID) {
-    // fp32: blocks of 32 rows x CW columns
+  if constexpr (EPI == EPI_RESID || EPI == EPI_PARTIAL) {
+    // fp32: blocks of 32 rows x CW columns (split-K partials go to their chunk's slice of X)
+    float* const xo = EPI == EPI_PARTIAL ? a.X + (size_t)split * a.M * a.ldx : a.X;
     constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
     float4 bb[FN][4] = {};
 #pragma unroll
@@ -668,7 +676,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
         const int c0 = cbase + cp * CW;
         flush(CPR, [&](int r) -> char* {
           const int m = rbase + i * 32 + r;
-          return m < a.M ? reinterpret_cast<char*>(a.X + (size_t)m * a.ldx + c0) : nullptr;
+          return m < a.M ? reinterpret_cast<char*>(xo + (size_t)m * a.ldx + c0) : nullptr;
         }, nchunks(a.N - c0, 4, CPR));
       }
   } else if constexpr (EPI == EPI_STORE || EPI == EPI_GEGLU) {
@@ -826,7 +834,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 // build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
 template <int BM, int BN, int WM, int WN, int EPI, int ACT>
 static void launch_xl_hb(const GemmArgs& a, hipStream_t st) {
-  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (EPI == EPI_PARTIAL ? a.ksplit : 1);
   if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true>), dim3(tiles), dim3(256), 0, st, a);
   else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false>), dim3(tiles), dim3(256), 0, st, a);
 }
@@ -846,6 +854,7 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
       else { fprintf(stderr, "[laya] gemm: QKV tiles need BM <= BN\n"); exit(1); }
       break;
     case EPI_GEGLU: launch_xl_hb<BM, BN, WM, WN, EPI_GEGLU, ACT_NONE>(a, st); break;
+    case EPI_PARTIAL: launch_xl_hb<BM, BN, WM, WN, EPI_PARTIAL, ACT_NONE>(a, st); break;
     default: fprintf(stderr, "[laya] gemm: bad epilogue %d\n", epi); exit(1);
   }
 }
@@ -892,6 +901,10 @@ int gemm_config(int cfg) {
   g_gemm_cfg.store(cfg, std::memory_order_relaxed);
   return prev;
 }
+
+static std::atomic<int> g_ksplit{0};
+
+int gemm_pin_ksplit(int ks) { return g_ksplit.exchange(ks, std::memory_order_relaxed); }
 
 void gemm_pin_split(int split_rows, int cfg_tail) {
   g_split_rows.store(split_rows, std::memory_order_relaxed);
@@ -989,6 +1002,80 @@ static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
   }
 }
 
+// Split-K reduction: out = epilogue(sum over the ks partial slices in slice order + bias), four
+// columns per thread.  EPI_RESID adds into the fp32 residual X; EPI_STORE applies the activation
+// and stores bf16.
+template <int EPI, int ACT, bool HB>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int ks, int M, int N,
+                                                       const float* __restrict__ bias, void* out, int ldo) {
+  const size_t n4 = (size_t)M * N / 4, slice = (size_t)M * N;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    const size_t e = i * 4;
+    const int m = (int)(e / N), n = (int)(e % N);
+    float4 v = *reinterpret_cast<const float4*>(ws + e);
+    for (int k = 1; k < ks; k++) {
+      const float4 t = *reinterpret_cast<const float4*>(ws + k * slice + e);
+      v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
+    }
+    if constexpr (HB) {
+      const float4 b = *reinterpret_cast<const float4*>(bias + n);
+      v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+    }
+    if constexpr (EPI == EPI_RESID) {
+      float4* xp = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + (size_t)m * ldo + n);
+      float4 x = *xp;
+      x.x += v.x; x.y += v.y; x.z += v.z; x.w += v.w;
+      *xp = x;
+    } else {
+      auto f = [](float t) {
+        if constexpr (ACT == ACT_RELU) t = fmaxf(t, 0.f);
+        if constexpr (ACT == ACT_GELU) t = gelu_erf_as(t);
+        return t;
+      };
+      uint2 u;
+      u.x = pk_bf16(f(v.x), f(v.y));
+      u.y = pk_bf16(f(v.z), f(v.w));
+      *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(out) + (size_t)m * ldo + n) = u;
+    }
+  }
+}
+
+template <int EPI, int ACT>
+static void launch_reduce(const GemmArgs& a, const float* ws, int ks, int M, void* out, int ldo, hipStream_t st) {
+  const size_t n4 = (size_t)M * a.N / 4;
+  const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+  if (a.bias) hipLaunchKernelGGL((k_splitk_reduce<EPI, ACT, true>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
+  else hipLaunchKernelGGL((k_splitk_reduce<EPI, ACT, false>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
+}
+
+// Split-K over rows chunks that fit the workspace: per chunk one launch of ks x tiles workgroups
+// writing fp32 partials (EPI_PARTIAL), then one reduction.
+static void launch_splitk(int epi, const GemmArgs& a, int ks, hipStream_t st) {
+  const size_t row_bytes = (size_t)ks * a.N * sizeof(float);
+  const int rc = (int)std::min<size_t>((size_t)a.M, a.ws_bytes / row_bytes);
+  if (rc < 1) { fprintf(stderr, "[laya] gemm: split-K workspace too small\n"); exit(1); }
+  for (int r0 = 0; r0 < a.M; r0 += rc) {
+    const int mr = std::min(rc, a.M - r0);
+    GemmArgs p = rows_from(a, r0);
+    p.M = mr;
+    p.K = a.K / ks;
+    p.bias = nullptr;
+    p.act = ACT_NONE;
+    p.X = a.ws;
+    p.ldx = a.N;
+    p.ksplit = ks;
+    launch_xl_cfg(EPI_PARTIAL, p, 3, st);                 // 128x128 tiles: the most workgroups
+    if (epi == EPI_RESID) {
+      launch_reduce<EPI_RESID, ACT_NONE>(a, a.ws, ks, mr, a.X + (size_t)r0 * a.ldx, a.ldx, st);
+    } else {
+      void* out = reinterpret_cast<bf16_t*>(a.C) + (size_t)r0 * a.ldc;
+      if (a.act == ACT_RELU) launch_reduce<EPI_STORE, ACT_RELU>(a, a.ws, ks, mr, out, a.ldc, st);
+      else if (a.act == ACT_GELU) launch_reduce<EPI_STORE, ACT_GELU>(a, a.ws, ks, mr, out, a.ldc, st);
+      else launch_reduce<EPI_STORE, ACT_NONE>(a, a.ws, ks, mr, out, a.ldc, st);
+    }
+  }
+}
+
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
   const char* why = "";
@@ -998,6 +1085,12 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
   }
   if constexpr (sizeof(T) == 2) {
     if (xl_usable(epi, a)) {
+      const int pinned_ks = g_ksplit.load(std::memory_order_relaxed);
+      const int ks = a.ksplit > 1 ? a.ksplit : pinned_ks;
+      if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % (ks * 32) == 0 && a.ws != nullptr) {
+        launch_splitk(epi, a, ks, st);
+        return;
+      }
       // a pinned configuration (LAYA_GEMM_CFG / gemm_config, with its pinned row split) wins over
       // the caller's, which wins over the planner's; one this shape cannot use falls through
       int cfg = a.cfg, split = a.split_rows, tail = a.cfg_tail;

@@ -25,7 +25,7 @@ HOST_LIB = os.path.join(PKG, "liblaya_host.so")
 ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act", "laya_max_len",
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
-               "laya_ext_gemm_config", "laya_ext_gemm_split"]
+               "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit"]
 
 _IP = ctypes.POINTER(ctypes.c_int)
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -75,6 +75,8 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_gemm_config.restype = ctypes.c_int
     L.laya_ext_gemm_split.argtypes = [ctypes.c_int, ctypes.c_int]
     L.laya_ext_gemm_split.restype = ctypes.c_int
+    L.laya_ext_gemm_ksplit.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    L.laya_ext_gemm_ksplit.restype = ctypes.c_int
     return L
 
 
@@ -104,6 +106,16 @@ def gemm_split(lib, split_rows: int, cfg_tail: int = -1):
     """Row split for pinned bf16 launches: rows [split_rows, M) in a second launch with cfg_tail."""
     if lib.laya_ext_gemm_split(split_rows, cfg_tail) != 0:
         raise ValueError("invalid GEMM split %d / %d" % (split_rows, cfg_tail))
+
+
+def gemm_ksplit(lib, ks: int, ws=None) -> int:
+    """Split-K factor for later bf16 GEMM hook calls (0: none) with workspace ws (a torch device
+    tensor); returns the previous factor."""
+    prev = lib.laya_ext_gemm_ksplit(ks, ws.data_ptr() if ws is not None else None,
+                                    ws.numel() * ws.element_size() if ws is not None else 0)
+    if prev == -2:
+        raise ValueError("invalid split-K factor %d" % ks)
+    return prev
 
 
 def _ptr(a: np.ndarray, ct):

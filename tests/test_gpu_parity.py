@@ -92,6 +92,20 @@ def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
         le.gemm_config(lib, prev)
 
 
+# split-K: K in ks chunks of fp32 partial products, summed in chunk order (bf16 operands)
+@pytest.mark.parametrize("ks", [2, 4, 8, 16])
+@pytest.mark.parametrize("M,N,K", [(160, 1024, 1024), (300, 384, 512), (1, 256, 4096), (1300, 512, 2048)])
+def test_gemm_split_k_vs_torch(ks, M, N, K):
+    import torch
+    lib = le.load_library()
+    ws = torch.empty(ks * min(M, 512) * N, dtype=torch.float32, device="cuda")   # rows in chunks of <= 512
+    prev = le.gemm_ksplit(lib, ks, ws)
+    try:
+        _check_gemm(lib, "bf16", M, N, K)
+    finally:
+        le.gemm_ksplit(lib, prev)
+
+
 def _check_gemm(lib, dtype, M, N, K):
     import torch
     g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
