@@ -222,9 +222,9 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 // ======================================================================================
 // bf16 attention (v_mfma_f32_32x32x16_bf16).  One 128-thread workgroup owns one query tile (<= 64
 // queries of one sequence) of one head; each of its two waves owns 32 queries, so every K and V^T
-// fragment read from LDS feeds a 32-query MFMA.  Keys advance in blocks of 64, double-buffered in
-// LDS: the block after the current one is fetched by LDS DMA (inline assembly, as in the GEMM)
-// while the current one is multiplied, with one wait and one barrier per block.
+// fragment read from LDS feeds a 32-query MFMA.  Keys advance in blocks of 64, fetched by LDS DMA
+// (inline assembly, as in the GEMM): the next block's K while the current block is scored, the next
+// block's V^T (one buffer) after the current PV step, each published by one wait and one barrier.
 //
 //   S^T[key][query] = K Q^T   A = K rows (32 keys x 16 d per MFMA), B = Q rows (registers)
 //   O^T[d][query] += V^T P^T  A = V^T rows (32 d x 16 keys),       B = P^T from the S^T registers
@@ -267,7 +267,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   // [buffer][row][8 chunks of 16 bytes]: K rows are keys, V^T rows are d; chunk c of row r sits at
   // position c ^ ((r >> 1) & 7), so 16 lanes reading one chunk of 16 consecutive rows hit 16
   // distinct 16-byte bank positions
-  __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs0[64 * 8], Vs1[64 * 8];
+  // K is double-buffered (the next block's K is fetched while the current one is used); V^T has
+  // one buffer, refilled right after the PV step and landing while the next block's scores and
+  // softmax run.  24 KB per workgroup: six workgroups (the VGPR limit) fit a CU.
+  __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs[64 * 8];
 
   // heads are the fastest grid dimension, so the (longest-first) tiles start in order
   const AttnTile tile = tiles[blockIdx.y];
@@ -316,12 +319,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     vvo[j] = ((uint32_t)(h * HD + row) * (uint32_t)ldv + (uint32_t)base) * 2u + (uint32_t)c * 16u;
   }
   const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 4u * 1024u;
-  auto fetch = [&](int k0, u32x4_t* ks, u32x4_t* vs) {
+  auto fetch_k = [&](int k0, u32x4_t* ks) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
-      attn_dma16(rV, lds_addr_a(vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
-    }
+    for (int j = 0; j < 4; j++) attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
+  };
+  auto fetch_v = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
   };
 
   f32x16_t o[2];
@@ -334,7 +338,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   float m_run = -INFINITY, l_run = 0.f;
   const float c2 = scale * 1.44269504088896340736f;
 
-  fetch(lo, Ks0, Vs0);
+  fetch_k(lo, Ks0);
+  fetch_v(lo);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
@@ -344,11 +349,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   for (int k0 = lo; k0 < hi_k; k0 += 64, ++it) {
     const bool odd = it & 1;
     const u32x4_t* ks = odd ? Ks1 : Ks0;
-    const u32x4_t* vs = odd ? Vs1 : Vs0;
-    if (k0 + 64 < hi_k) {
-      if (odd) fetch(k0 + 64, Ks0, Vs0);
-      else fetch(k0 + 64, Ks1, Vs1);
-    }
+    const u32x4_t* vs = Vs;
+    const bool more = k0 + 64 < hi_k;
+    // the other K buffer was last read by the previous block's scores, before its final barrier
+    if (more) fetch_k(k0 + 64, odd ? Ks0 : Ks1);
 
     // ---- S^T = K Q^T: two 32-key sub-blocks ----
     f32x16_t st[2];
@@ -406,6 +410,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     l_run += rs;
     m_run = m_new;
 
+    // this block's V^T (fetched after the previous PV step, before the K fetch above) has landed
+    // in every wave's part
+    if (more) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
     // ---- O^T += V^T P^T: four 16-key steps ----
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
@@ -425,10 +436,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pb, o[db], 0, 0, 0);
       }
     }
-    // the next block has landed (this wave's part) and no wave still reads the current buffers
+    // the next block's K has landed (this wave's part) and no wave still reads V^T or this K
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if (more) fetch_v(k0 + 64);
   }
 
   if (!qvalid) return;
