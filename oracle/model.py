@@ -39,7 +39,7 @@ import torch.nn.functional as F
 
 
 def _t(w, dtype):
-    return w if isinstance(w, torch.Tensor) and w.dtype == dtype else torch.as_tensor(np.asarray(w)).to(dtype)
+    return w if isinstance(w, torch.Tensor) and w.dtype == dtype else torch.as_tensor(np.require(w, requirements='W')).to(dtype)
 
 
 class Weights:
