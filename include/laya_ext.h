@@ -50,7 +50,7 @@ int laya_ext_gemm_config(int cfg);
 int laya_ext_gemm_split(int split_rows, int cfg_tail);
 
 /* Split-K factor (0 or 1: none, up to 64) for later bf16 laya_ext_gemm calls, process-wide: K is
- * cut into that many chunks (K must be a multiple of 32 * ks, else the call runs unsplit) whose
+ * cut into that many chunks (K must be a multiple of 64 * ks, else the call runs unsplit) whose
  * fp32 partial products go to the caller's device workspace ws (ws_bytes; rows are processed in
  * chunks that fit it) and are summed in chunk order.  The engine uses it for its GEMMs on the
  * gathered head rows and the scorer.  Returns the previous factor, or -2 for an invalid value. */

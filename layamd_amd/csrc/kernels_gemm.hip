@@ -6,8 +6,9 @@
 // transposed.  Two kernels:
 //
 //   k_gemm_xl  bf16, the engine's path.  256-thread workgroups, tiles from 128x128 to 256x256 on
-//              v_mfma_f32_32x32x16_bf16; K advances in 32-deep slices through five LDS stages
-//              filled four slices ahead by LDS DMA (buffer_load ... lds); the product is computed
+//              v_mfma_f32_32x32x16_bf16; K advances in 64-deep stages (whole 128-byte lines of
+//              every tile row), two in LDS, filled one ahead by LDS DMA (buffer_load ... lds);
+//              the product is computed
 //              transposed so each lane holds four consecutive output columns; the epilogue is
 //              staged through LDS and leaves as full-line 16-byte stores.  The engine picks the
 //              tile shape (and an optional row split over two launches) per GEMM by timing.
@@ -278,7 +279,8 @@ __device__ __forceinline__ uint32_t pair_rows_to_cols(float ve, float ve1, bool 
 
 // ======================================================================================
 // Large-tile bf16 GEMM (v_mfma_f32_32x32x16_bf16).  A workgroup of 4 wave64s computes a
-// BM x BN tile (256x256 by default, one workgroup per CU, 128 KiB of LDS for two K stages);
+// BM x BN tile (256x256 by default, one workgroup per CU, 128 KiB of LDS for two K stages and
+// 32 KiB for the epilogue's staging);
 // each wave owns a (BM/WM) x (BN/WN) sub-tile held in 32x32 accumulator blocks, so one
 // 16-byte LDS fragment feeds 4 MFMAs and LDS traffic stays well under the MFMA rate.
 // Global loads go through buffer resources: rows beyond M (or N) fall outside the resource and
@@ -328,88 +330,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// LDS fill by DMA: each wave instruction fills 64 consecutive 16-byte chunks = 16 tile rows of
-// one 32-deep K slice (64 bytes per row).  The swizzle is applied on the global side: the lane
-// landing at row r, chunk position c loads global chunk c ^ f(r), f(r) = ((r >> 1) & 3) ^
-// ((r >> 3) & 1).  A fragment read has lane l on row l % 32 at one logical chunk; with 64 banks of
-// 4 bytes each group of 16 lanes then covers 16 distinct 16-byte bank positions ((r & 3) * 4 +
-// (k ^ f(r)) over r = 0..15), and each group of 8 covers 8 of 8 with 32 banks, so the reads are
-// conflict-free.  The per-lane offset (row * ld + swizzled chunk) is fixed over K; the slice's K
-// byte offset goes in the scalar offset.  Rows past M (or N) are out of range by the per-lane
-// offset alone and arrive as zeros; a slice past the last one is fetched through a resource of
-// zero length, so it reads nothing.
-__device__ __forceinline__ uint32_t dma_voff(int row0, int r, int ld_bytes, int lane) {
-  const int cpos = lane & 3;
-  return (uint32_t)(row0 + r) * (uint32_t)ld_bytes + ((uint32_t)(cpos ^ ((r >> 1) & 3) ^ ((r >> 3) & 1)) << 4);
-}
-
-// Fragments of one 16-deep K step: lane l holds 8 consecutive K values (16 bytes) of tile row
-// (row base + 32 i + l % 32), K offset 8 * (l / 32); ks selects the step within the 32-deep slice.
+// Fragments of one 16-deep K sub-step: lane l holds 8 consecutive K values (16 bytes) of tile row
+// (row base + 32 i + l % 32), K offset 8 * (l / 32).
 template <int FM, int FN>
 struct Frags {
   u32x4_t a[FM], b[FN];
 };
 
-template <int FM, int FN>
-__device__ __forceinline__ void load_frags(Frags<FM, FN>& f, const u32x4_t* As, const u32x4_t* Bs, int arow, int brow,
-                                           int ks, int hi, int sw) {
-#pragma unroll
-  for (int i = 0; i < FM; i++) f.a[i] = As[(arow + i * 32) * 4 + ((2 * ks + hi) ^ sw)];
-#pragma unroll
-  for (int j = 0; j < FN; j++) f.b[j] = Bs[(brow + j * 32) * 4 + ((2 * ks + hi) ^ sw)];
-}
-
-template <int FM, int FN>
-__device__ __forceinline__ void mma_frags(f32x16_t (&acc)[FM][FN], const Frags<FM, FN>& f) {
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]),
-                                                          __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
-}
-
-// single-fragment and single-MFMA forms of the above, for interleaved issue
-template <int FM, int FN>
-__device__ __forceinline__ void load_frag(Frags<FM, FN>& f, int idx, const u32x4_t* As, const u32x4_t* Bs, int arow,
-                                          int brow, int ks, int hi, int sw) {
-  if (idx < FM) f.a[idx] = As[(arow + idx * 32) * 4 + ((2 * ks + hi) ^ sw)];
-  else f.b[idx - FM] = Bs[(brow + (idx - FM) * 32) * 4 + ((2 * ks + hi) ^ sw)];
-}
-
-template <int FM, int FN>
-__device__ __forceinline__ void mma_one(f32x16_t (&acc)[FM][FN], const Frags<FM, FN>& f, int t) {
-  const int i = t / FN, j = t % FN;
-  acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, f.a[i]), __builtin_bit_cast(bf16x8_t, f.b[j]),
-                                                      acc[i][j], 0, 0, 0);
-}
-
 // s_waitcnt vmcnt(n) lgkmcnt(0): all but this wave's n most recent vector-memory instructions
 // (here: DMA fills) have completed, and so have all of its LDS reads.  Placed before each barrier:
 // after it, no wave has an LDS read of an older stage in flight.
 #define LAYA_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(n) : "memory")
-
-// DMA plan of one workgroup: resources of A and W (and one of zero length for slices past the
-// last), the per-lane offsets of this wave's PA + PB instructions per slice (A rows, then W rows)
-// and the wave's byte offset inside each stage part.
-template <int PA, int PB>
-struct XlDma {
-  u32x4_t rA, rB, rNone;
-  uint32_t voff[PA + PB];
-  uint32_t wsa, wsb;
-  int nk;
-  template <class ST>
-  __device__ __forceinline__ void op(int o, ST& S, int kt) const {
-    const bool live = kt < nk;
-    if (o < PA) dma16(live ? rA : rNone, lds_addr(S.a) + wsa + o * 1024, voff[o], (uint32_t)kt * 64u);
-    else dma16(live ? rB : rNone, lds_addr(S.b) + wsb + (o - PA) * 1024, voff[o], (uint32_t)kt * 64u);
-  }
-  template <class ST>
-  __device__ __forceinline__ void slice(ST& S, int kt) const {
-#pragma unroll
-    for (int o = 0; o < PA + PB; o++) op(o, S, kt);
-  }
-};
 
 // acc[i][j] += A block i . W block j^T (SWAP: the transposed product W block j . A block i^T,
 // whose accumulator layout gives each lane 4 consecutive output columns of one row)
@@ -424,78 +355,115 @@ __device__ __forceinline__ void mma_one_x(f32x16_t (&acc)[FM][FN], const Frags<F
                                                         __builtin_bit_cast(bf16x8_t, f.b[j]), acc[i][j], 0, 0, 0);
 }
 
-// The K loop of one tile.  Slice s (32 deep) is fetched into stage s % 5 four steps ahead; slices
-// 0..3 were issued by the caller.  Step kt multiplies the two 16-deep halves of slice kt from
-// registers (F0, F1) while loading the next half: F1 (slice kt, second half) during the first, F0
-// (slice kt + 1, first half) during the second.  Between the halves each wave waits for its own
-// part of slice kt + 1 (two later slices may stay in flight), then the barrier makes slice kt + 1
-// visible to all waves and frees stage (kt - 1) % 5, whose last reads (F1 of slice kt - 1) were
-// consumed before every wave reached it; the refill of that stage with slice kt + 4 follows.  Every
-// step issues the same number of DMA instructions (past the last slice they read nothing), so the
-// wait count is constant.  With one or two waves per SIMD the MFMA pipe idles whenever a wave issues
-// anything else, so the DMA instructions and the fragment loads of the next half are spread between
-// the MFMAs of the current one (first half: DMA then F0 loads; second half: F1 loads), each MFMA
-// followed by its share, fixed by scheduling fences.
-template <bool SWAP, int FM, int FN, int PA, int PB, class ST>
-__device__ __forceinline__ void xl_k_loop(f32x16_t (&acc)[FM][FN], ST& S0, ST& S1, ST& S2, ST& S3, ST& S4,
-                                          const XlDma<PA, PB>& d, int arow, int brow, int hi, int sw) {
-  constexpr int PS = PA + PB, NMM = FM * FN, E1 = PA + PB + FM + FN, E2 = FM + FN;
-  const int nk = d.nk;
-  Frags<FM, FN> F0, F1;
-  LAYA_WAIT_VMCNT(3 * PS);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  load_frags(F0, S0.a, S0.b, arow, brow, 0, hi, sw);
-  load_frags(F1, S0.a, S0.b, arow, brow, 1, hi, sw);
+// ---- 64-deep stages: one whole 128-byte line of every tile row per stage ----
+// A 32-deep K slice would use 64 bytes of each 128-byte line, and the other half of the line (the
+// next slice) is no longer in the CU's 32 KB L1 when it is asked for, so each half line would cost
+// a whole-line L2 request.  A stage of 64 K values per row fetches each line once.
+//
+// Stage rows are 128 bytes (8 chunks of 16 bytes); the chunk at slot c of row r holds logical chunk
+// c ^ g(r), g(r) = (r & 7) ^ ((r >> 3) & 1).  A fragment read has lane l on row l % 32 at one
+// logical chunk: a group of 16 lanes (rows r0..r0+15) covers 16 distinct 16-byte positions of the
+// 256 bytes that 64 banks span (even and odd rows each see 8 distinct g), and a group of 8 covers
+// the 8 positions of 32 banks, so the reads are conflict-free.  One DMA instruction fills 8 rows:
+// lane l writes row 8 q + l / 8 (q = instruction index within the stage part), slot l % 8.
+__device__ __forceinline__ uint32_t dma64_voff(int row0, int r8, int ld_bytes, int lane, int odd) {
+  const int rl = lane >> 3;
+  return (uint32_t)(row0 + r8 + rl) * (uint32_t)ld_bytes + ((uint32_t)((lane & 7) ^ rl ^ odd) << 4);
+}
+
+// DMA plan of one workgroup for 64-deep stages: PA + PB instructions per wave and stage.  The
+// per-lane offset depends only on the parity of the instruction index (the swizzle's row term);
+// the instruction's row step and the stage's K offset go in the scalar offset.
+template <int PA, int PB>
+struct XlDma64 {
+  u32x4_t rA, rB, rNone;
+  uint32_t va[2], vb[2];
+  uint32_t wsa, wsb;
+  int lda8, ldw8;   // bytes of 8 rows
+  int ns;           // 32-deep slices (even: whole 64-deep stages)
+  template <class ST>
+  __device__ __forceinline__ void op(int o, ST& S, int g) const {
+    const bool live = 2 * g < ns;
+    if (o < PA) dma16(live ? rA : rNone, lds_addr(S.a) + wsa + o * 1024, va[o & 1], (uint32_t)g * 128u + (uint32_t)(o * lda8));
+    else dma16(live ? rB : rNone, lds_addr(S.b) + wsb + (o - PA) * 1024, vb[(o - PA) & 1], (uint32_t)g * 128u + (uint32_t)((o - PA) * ldw8));
+  }
+  template <class ST>
+  __device__ __forceinline__ void stage(ST& S, int g) const {
 #pragma unroll
-  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F0, t);
-  LAYA_WAIT_VMCNT(2 * PS);
+    for (int o = 0; o < PA + PB; o++) op(o, S, g);
+  }
+};
+
+// fragment idx (A blocks, then W blocks) of 16-deep sub-step s of a 64-deep stage
+template <int FM, int FN>
+__device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32x4_t* As, const u32x4_t* Bs, int arow,
+                                            int brow, int s, int hi, int sw) {
+  if (idx < FM) f.a[idx] = As[(arow + idx * 32) * 8 + ((2 * s + hi) ^ sw)];
+  else f.b[idx - FM] = Bs[(brow + (idx - FM) * 32) * 8 + ((2 * s + hi) ^ sw)];
+}
+
+// The K loop over 64-deep stages in two LDS buffers.  Stages 0 and 1 were issued by the caller.
+// Stage g runs four 16-deep sub-steps, each multiplying one register set while the other is
+// loaded with the next sub-step's fragments.  After the third sub-step's
+// fragment loads every wave has all of stage g in registers; one wait and one barrier then publish
+// stage g + 1 and free stage g's buffer, which is refilled with stage g + 2 between the fourth
+// sub-step's MFMAs, together with the loads of stage g + 1's first fragments.  One stage is in
+// flight while another is multiplied; every stage but the last issues the same DMA instructions
+// (past the last stage they read nothing), so the wait is a constant vmcnt(0).  K is a multiple of
+// 64 (every stage is whole).
+template <bool SWAP, int FM, int FN, int PA, int PB, class ST>
+__device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST& T1, const XlDma64<PA, PB>& d, int arow,
+                                            int brow, int hi, int sw) {
+  constexpr int PS = PA + PB, NMM = FM * FN, E = FM + FN, E1 = PS + FM + FN;
+  Frags<FM, FN> F0, F1;
+  LAYA_WAIT_VMCNT(PS);                     // stage 0 (stage 1 may still be in flight)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  // one step, from the barrier that published slice kt to the one that publishes slice kt + 1
-#define LAYA_GEMM_STEP(SN, SR)                                                            \
+#pragma unroll
+  for (int o = 0; o < E; o++) load_frag64(F0, o, T0.a, T0.b, arow, brow, 0, hi, sw);
+  // MFMAs of register set FX, with the loads of sub-step s of stage SL into FY spread between them
+#define LAYA_SUB64(FX, FY, SL, s)                                                         \
+  _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                       \
+    mma_one_x<SWAP>(acc, FX, t);                                                          \
+    _Pragma("unroll") for (int o = t * E / NMM; o < (t + 1) * E / NMM; o++)              \
+      load_frag64(FY, o, SL.a, SL.b, arow, brow, s, hi, sw);                              \
+    __builtin_amdgcn_sched_barrier(0);                                                    \
+  }
+  // stage g in buffer C, followed by stage g + 1 in buffer N
+#define LAYA_STAGE64(C, N)                                                                \
   {                                                                                       \
+    LAYA_SUB64(F0, F1, C, 1)                                                              \
+    LAYA_SUB64(F1, F0, C, 2)                                                              \
+    LAYA_SUB64(F0, F1, C, 3)                                                              \
+    LAYA_WAIT_VMCNT(0);                                                                   \
+    __builtin_amdgcn_s_barrier();                                                         \
+    asm volatile("" ::: "memory");                                                        \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
       mma_one_x<SWAP>(acc, F1, t);                                                        \
       _Pragma("unroll") for (int o = t * E1 / NMM; o < (t + 1) * E1 / NMM; o++) {        \
-        if (o < PA + PB) d.op(o, SR, kt + 4);                                             \
-        else load_frag(F0, o - PA - PB, SN.a, SN.b, arow, brow, 0, hi, sw);               \
+        if (o < PS) d.op(o, C, g + 2);                                                    \
+        else load_frag64(F0, o - PS, N.a, N.b, arow, brow, 0, hi, sw);                    \
       }                                                                                   \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
-    ++kt;                                                                                 \
-    _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
-      mma_one_x<SWAP>(acc, F0, t);                                                        \
-      _Pragma("unroll") for (int o = t * E2 / NMM; o < (t + 1) * E2 / NMM; o++)          \
-        load_frag(F1, o, SN.a, SN.b, arow, brow, 1, hi, sw);                              \
-      __builtin_amdgcn_sched_barrier(0);                                                  \
-    }                                                                                     \
-    LAYA_WAIT_VMCNT(2 * PS);                                                              \
-    __builtin_amdgcn_s_barrier();                                                         \
-    asm volatile("" ::: "memory");                                                        \
+    ++g;                                                                                  \
   }
-  int kt = 0;                              // slice whose first half has been multiplied
-  for (; kt + 6 <= nk;) {                  // five whole steps, the last one loading slice kt + 5
-    LAYA_GEMM_STEP(S1, S4)
-    LAYA_GEMM_STEP(S2, S0)
-    LAYA_GEMM_STEP(S3, S1)
-    LAYA_GEMM_STEP(S4, S2)
-    LAYA_GEMM_STEP(S0, S3)
+  const int nst = d.ns / 2;                // stages
+  int g = 0;
+  for (; g + 2 < nst;) {                   // two stages, each followed by another
+    LAYA_STAGE64(T0, T1)
+    LAYA_STAGE64(T1, T0)
   }
-  if (kt + 1 < nk) {                       // at most four whole steps remain
-    LAYA_GEMM_STEP(S1, S4)
-    if (kt + 1 < nk) {
-      LAYA_GEMM_STEP(S2, S0)
-      if (kt + 1 < nk) {
-        LAYA_GEMM_STEP(S3, S1)
-        if (kt + 1 < nk) LAYA_GEMM_STEP(S4, S2)
-      }
-    }
-  }
-#undef LAYA_GEMM_STEP
+  if (g + 2 == nst) LAYA_STAGE64(T0, T1)   // g is even: stage g in T0; the last one is in T1
+  ST& L = (g & 1) ? T1 : T0;               // the last stage (g == nst - 1)
+  LAYA_SUB64(F0, F1, L, 1)
+  LAYA_SUB64(F1, F0, L, 2)
+  LAYA_SUB64(F0, F1, L, 3)
 #pragma unroll
-  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);   // second half of the last slice
-  LAYA_WAIT_VMCNT(0);                                            // the refills past the last slice
+  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);
+#undef LAYA_STAGE64
+#undef LAYA_SUB64
+  LAYA_WAIT_VMCNT(0);                      // the refills past the last slice
 }
 
 template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB>
@@ -503,16 +471,20 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  // the A part of a stage holds BM rounded up to whole DMA instructions (64 rows over the 4 waves);
-  // rows BM.. of it are fetched (the next tile's rows, or zeros past M) and never read
-  constexpr int BMP = (BM + 63) / 64 * 64;
-  constexpr int PA = BMP / 64, PB = BN / 64;             // DMA instructions per wave and slice
+  // the A part of a stage holds BM rounded up to whole DMA instructions (32 rows over the 4 waves)
+  constexpr int BMQ = (BM + 31) / 32 * 32;
+  constexpr int PA = BMQ / 32, PB = BN / 32;             // DMA instructions per wave and stage
   static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0 && BN % 64 == 0, "tile");
-  // five 32-deep K stages ((BMP + BN) * 64 bytes each), separate objects so the compiler sees that
-  // the DMA into one stage and the fragment reads of another never alias
+  static_assert(PA % 2 == 0 && PB % 2 == 0, "swizzle parity: even instruction count per wave");
+  // two 64-deep K stages ((BMQ + BN) * 128 bytes each) and the epilogue's staging area, separate
+  // objects so the compiler sees that the DMA into one stage and the fragment reads of another
+  // never alias
+  constexpr int BMP = (BM + 63) / 64 * 64;
+  struct Stage64 { u32x4_t a[BMQ * 8]; u32x4_t b[BN * 8]; };
   struct Stage { u32x4_t a[BMP * 4]; u32x4_t b[BN * 4]; };
-  __shared__ Stage S0, S1, S2, S3, S4;
-  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BMP + BN) * 64, "RoPE tables: one stage each for cos and sin");
+  __shared__ Stage64 T0, T1;
+  __shared__ Stage S4;
+  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BMQ + BN) * 128, "RoPE tables: one stage each for cos and sin");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -544,23 +516,23 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     }
   }
 
-  XlDma<PA, PB> dm;
+  XlDma64<PA, PB> dm;
   const size_t k0 = (size_t)split * a.K;                 // first K column of this workgroup
   dm.rA = make_rsrc(reinterpret_cast<const T*>(a.A) + k0, (uint32_t)(((size_t)a.M * a.lda - k0) * sizeof(T)));
   dm.rB = make_rsrc(reinterpret_cast<const T*>(a.W) + k0, (uint32_t)(((size_t)a.N * a.ldw - k0) * sizeof(T)));
   dm.rNone = make_rsrc(a.A, 0u);           // zero length: every offset out of range
   const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
-#pragma unroll
-  for (int o = 0; o < PA + PB; o++)
-    dm.voff[o] = o < PA ? dma_voff(m0, (wave * PA + o) * 16 + (lane >> 2), lda_b, lane)
-                        : dma_voff(n0, (wave * PB + o - PA) * 16 + (lane >> 2), ldw_b, lane);
+  dm.va[0] = dma64_voff(m0, wave * PA * 8, lda_b, lane, 0);
+  dm.va[1] = dma64_voff(m0, wave * PA * 8, lda_b, lane, 1);
+  dm.vb[0] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 0);
+  dm.vb[1] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 1);
   dm.wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
   dm.wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
-  dm.nk = a.K / 32;
-  dm.slice(S0, 0);
-  dm.slice(S1, 1);
-  dm.slice(S2, 2);
-  dm.slice(S3, 3);
+  dm.lda8 = 8 * lda_b;
+  dm.ldw8 = 8 * ldw_b;
+  dm.ns = a.K / 32;
+  dm.stage(T0, 0);
+  dm.stage(T1, 1);
 
   // Output coordinates.  Transposed product: lane holds, for block (i, j) and element e, output row
   // rbase + 32 i + lane % 32 and columns cbase + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4, i.e. four
@@ -598,15 +570,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   }
 
   const int arow = wm * WTM + l32, brow = wn * WTN + l32;
-  const int sw = ((lane >> 1) & 3) ^ ((lane >> 3) & 1);   // f(row) of fragment rows 32 n + lane % 32
-  if (swap) xl_k_loop<true>(acc, S0, S1, S2, S3, S4, dm, arow, brow, hi, sw);
-  else xl_k_loop<false>(acc, S0, S1, S2, S3, S4, dm, arow, brow, hi, sw);
+  const int sw = (lane & 7) ^ ((lane >> 3) & 1);          // g(row) of fragment rows 32 n + lane % 32
+  if (swap) xl_k_loop64<true>(acc, T0, T1, dm, arow, brow, hi, sw);
+  else xl_k_loop64<false>(acc, T0, T1, dm, arow, brow, hi, sw);
 
   // ---------------- epilogue ----------------
   // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
-  // writes the block (bias, activation, GeGLU, RoPE applied in registers) into its quarter of stage
-  // 4 as rows of 16-byte chunks, swizzled by row, then streams whole rows out with 16-byte stores
-  // (full cache lines).  Stages 0-3 stay free (they hold the RoPE tables for the QKV projection).
+  // writes the block (bias, activation, GeGLU, RoPE applied in registers) into its quarter of the
+  // staging area as rows of 16-byte chunks, swizzled by row, then streams whole rows out with
+  // 16-byte stores (full cache lines).  The K stages hold the RoPE tables for the QKV projection.
   // All global loads are issued before the first store: on gfx9 vmcnt counts stores too, so a load
   // issued after a store would wait for it.
   __syncthreads();                                        // every wave is done with the K stages
@@ -731,8 +703,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       constexpr int CW = fitw(WTN, SB / 64), CPR = CW / 8;
       static_assert(CW % 64 == 0, "whole heads per staged block");
       const bool rope = a.rope_cos != nullptr;
-      float* tcos = reinterpret_cast<float*>(&S0);
-      float* tsin = reinterpret_cast<float*>(&S1);
+      float* tcos = reinterpret_cast<float*>(&T0);
+      float* tsin = reinterpret_cast<float*>(&T1);
       if (rope) {
         // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
         // four 16-byte pieces per thread at a time (the positions were loaded before the K loop)
@@ -1087,7 +1059,7 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     if (xl_usable(epi, a)) {
       const int pinned_ks = g_ksplit.load(std::memory_order_relaxed);
       const int ks = a.ksplit > 1 ? a.ksplit : pinned_ks;
-      if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % (ks * 32) == 0 && a.ws != nullptr) {
+      if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % (ks * 64) == 0 && a.ws != nullptr) {
         launch_splitk(epi, a, ks, st);
         return;
       }
