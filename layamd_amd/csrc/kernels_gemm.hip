@@ -381,16 +381,12 @@ struct XlDma64 {
   uint32_t wsa, wsb;
   int lda8, ldw8;   // bytes of 8 rows
   int ns;           // 32-deep slices (even: whole 64-deep stages)
-  template <class ST>
-  __device__ __forceinline__ void op(int o, ST& S, int g) const {
-    const bool live = 2 * g < ns;
-    if (o < PA) dma16(live ? rA : rNone, lds_addr(S.a) + wsa + o * 1024, va[o & 1], (uint32_t)g * 128u + (uint32_t)(o * lda8));
-    else dma16(live ? rB : rNone, lds_addr(S.b) + wsb + (o - PA) * 1024, vb[(o - PA) & 1], (uint32_t)g * 128u + (uint32_t)((o - PA) * ldw8));
+  // instruction o of the A (W) part of stage g, into the buffer at LDS byte address la (lb)
+  __device__ __forceinline__ void op_a(int o, uint32_t la, int g) const {
+    dma16(2 * g < ns ? rA : rNone, la + wsa + o * 1024, va[o & 1], (uint32_t)g * 128u + (uint32_t)(o * lda8));
   }
-  template <class ST>
-  __device__ __forceinline__ void stage(ST& S, int g) const {
-#pragma unroll
-    for (int o = 0; o < PA + PB; o++) op(o, S, g);
+  __device__ __forceinline__ void op_b(int o, uint32_t lb, int g) const {
+    dma16(2 * g < ns ? rB : rNone, lb + wsb + o * 1024, vb[o & 1], (uint32_t)g * 128u + (uint32_t)(o * ldw8));
   }
 };
 
@@ -402,7 +398,8 @@ __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32
   else f.b[idx - FM] = Bs[(brow + (idx - FM) * 32) * 8 + ((2 * s + hi) ^ sw)];
 }
 
-// The K loop over 64-deep stages in two LDS buffers.  Stages 0 and 1 were issued by the caller.
+// The K loop over 64-deep stages in two LDS buffers (one workgroup per CU: a stage's MFMAs cover
+// the fill of the next one).  Stages 0 and 1 were issued by the caller.
 // Stage g runs four 16-deep sub-steps, each multiplying one register set while the other is
 // loaded with the next sub-step's fragments.  After the third sub-step's
 // fragment loads every wave has all of stage g in registers; one wait and one barrier then publish
@@ -441,7 +438,8 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
       mma_one_x<SWAP>(acc, F1, t);                                                        \
       _Pragma("unroll") for (int o = t * E1 / NMM; o < (t + 1) * E1 / NMM; o++) {        \
-        if (o < PS) d.op(o, C, g + 2);                                                    \
+        if (o < PA) d.op_a(o, lds_addr(C.a), g + 2);                                      \
+        else if (o < PS) d.op_b(o - PA, lds_addr(C.b), g + 2);                            \
         else load_frag64(F0, o - PS, N.a, N.b, arow, brow, 0, hi, sw);                    \
       }                                                                                   \
       __builtin_amdgcn_sched_barrier(0);                                                  \
@@ -463,10 +461,86 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
   for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);
 #undef LAYA_STAGE64
 #undef LAYA_SUB64
-  LAYA_WAIT_VMCNT(0);                      // the refills past the last slice
+  LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB>
+
+// The K loop over 64-deep stages for two workgroups per CU, whose interleaved stages take twice
+// as long in wall time, so one stage in flight no longer covers a fill.  The A parts of stages
+// rotate through three LDS buffers and the W parts through two (A rows miss L2 more often than W
+// columns, which every row tile shares), in one array L: A buffer i at L + i * SA, W buffer j at L + 3 SA + j * SW.  The caller issued W 0,
+// A 0, W 1, A 1 and A 2, in that order.  Stage g runs four 16-deep sub-steps, each multiplying one
+// register set while the other is loaded with the next sub-step's fragments.  After the third
+// sub-step's fragment loads every wave has all of stage g in registers; one wait and one barrier
+// then publish stage g + 1 and free stage g's buffers, which are refilled between the fourth
+// sub-step's MFMAs with W of stage g + 2 and then A of stage g + 3, together with the loads of
+// stage g + 1's first fragments.  Loads complete in issue order, so the wait for stage g + 1 lets
+// exactly the A part of stage g + 2 stay in flight: vmcnt(PA).  Every stage but the last issues the
+// same DMA instructions (past the last stage they read nothing).  K is a multiple of 64.
+template <bool SWAP, int FM, int FN, int PA, int PB, int SA, int SW>
+__device__ __forceinline__ void xl_k_loop64r(f32x16_t (&acc)[FM][FN], const u32x4_t* L, const XlDma64<PA, PB>& d,
+                                             int arow, int brow, int hi, int sw) {
+  constexpr int PS = PA + PB, NMM = FM * FN, E = FM + FN, E1 = PS + FM + FN, OB = 3 * SA;
+  const uint32_t l0 = lds_addr(L);
+  Frags<FM, FN> F0, F1;
+  LAYA_WAIT_VMCNT(PB + 2 * PA);            // stage 0 (W 1, A 1 and A 2 may still be in flight)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int o = 0; o < E; o++) load_frag64(F0, o, L, L + OB, arow, brow, 0, hi, sw);
+  // MFMAs of register set FX, with the loads of sub-step s of the stage in (CA, CB) into FY spread
+  // between them
+#define LAYA_SUB64(FX, FY, CA, CB, s)                                                     \
+  _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                       \
+    mma_one_x<SWAP>(acc, FX, t);                                                          \
+    _Pragma("unroll") for (int o = t * E / NMM; o < (t + 1) * E / NMM; o++)              \
+      load_frag64(FY, o, CA, CB, arow, brow, s, hi, sw);                                  \
+    __builtin_amdgcn_sched_barrier(0);                                                    \
+  }
+  const int nst = d.ns / 2;                // stages
+  int ia = 0, ib = 0;                      // buffers of stage g
+  for (int g = 0; g + 1 < nst; g++) {
+    const int ia1 = ia == 2 ? 0 : ia + 1, ib1 = ib ^ 1;
+    const u32x4_t* CA = L + ia * SA;
+    const u32x4_t* CB = L + OB + ib * SW;
+    const u32x4_t* NA = L + ia1 * SA;
+    const u32x4_t* NB = L + OB + ib1 * SW;
+    LAYA_SUB64(F0, F1, CA, CB, 1)
+    LAYA_SUB64(F1, F0, CA, CB, 2)
+    LAYA_SUB64(F0, F1, CA, CB, 3)
+    LAYA_WAIT_VMCNT(PA);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint32_t la = l0 + (uint32_t)(ia * SA * 16), lb = l0 + (uint32_t)((OB + ib * SW) * 16);
+#pragma unroll
+    for (int t = 0; t < NMM; t++) {
+      mma_one_x<SWAP>(acc, F1, t);
+#pragma unroll
+      for (int o = t * E1 / NMM; o < (t + 1) * E1 / NMM; o++) {
+        if (o < PB) d.op_b(o, lb, g + 2);
+        else if (o < PS) d.op_a(o - PB, la, g + 3);
+        else load_frag64(F0, o - PS, NA, NB, arow, brow, 0, hi, sw);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    ia = ia1;
+    ib = ib1;
+  }
+  {                                        // the last stage
+    const u32x4_t* CA = L + ia * SA;
+    const u32x4_t* CB = L + OB + ib * SW;
+    LAYA_SUB64(F0, F1, CA, CB, 1)
+    LAYA_SUB64(F1, F0, CA, CB, 2)
+    LAYA_SUB64(F0, F1, CA, CB, 3)
+  }
+#pragma unroll
+  for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);
+#undef LAYA_SUB64
+  LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
+}
+
+// RING: the three-A-buffer K loop, for 128x128 tiles when the grid puts two workgroups on a CU
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, bool RING>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -476,15 +550,16 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   constexpr int PA = BMQ / 32, PB = BN / 32;             // DMA instructions per wave and stage
   static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0 && BN % 64 == 0, "tile");
   static_assert(PA % 2 == 0 && PB % 2 == 0, "swizzle parity: even instruction count per wave");
-  // two 64-deep K stages ((BMQ + BN) * 128 bytes each) and the epilogue's staging area, separate
-  // objects so the compiler sees that the DMA into one stage and the fragment reads of another
-  // never alias
+  // K stages: two whole stages (A then W part), or (RING) three A buffers and two W buffers (BMQ and
+  // BN rows of 128 bytes); after the K loop the same memory holds the epilogue's staging area (SB
+  // bytes per wave) and, for the QKV projection, the RoPE tables of the tile's rows
+  static_assert(!RING || BM * BN <= 128 * 128, "the ring loop is for two workgroups per CU");
+  constexpr int SA = BMQ * 8, SW = BN * 8;               // buffer sizes in 16-byte chunks
+  struct Stage64 { u32x4_t a[SA]; u32x4_t b[SW]; };
+  __shared__ u32x4_t L[RING ? 3 * SA + 2 * SW : 2 * (SA + SW)];
   constexpr int BMP = (BM + 63) / 64 * 64;
-  struct Stage64 { u32x4_t a[BMQ * 8]; u32x4_t b[BN * 8]; };
-  struct Stage { u32x4_t a[BMP * 4]; u32x4_t b[BN * 4]; };
-  __shared__ Stage64 T0, T1;
-  __shared__ Stage S4;
-  static_assert(EPI != EPI_QKV || BM * 32 * 4 <= (BMQ + BN) * 128, "RoPE tables: one stage each for cos and sin");
+  constexpr int SB = (BMP + BN) * 16;                    // staging bytes per wave
+  static_assert(4 * SB + (EPI == EPI_QKV ? 2 * BM * 32 * 4 : 0) <= (int)sizeof(L), "epilogue LDS");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -531,8 +606,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   dm.lda8 = 8 * lda_b;
   dm.ldw8 = 8 * ldw_b;
   dm.ns = a.K / 32;
-  dm.stage(T0, 0);
-  dm.stage(T1, 1);
+  Stage64& T0 = *reinterpret_cast<Stage64*>(L);
+  Stage64& T1 = *reinterpret_cast<Stage64*>(L + SA + SW);
+  if constexpr (!RING) {
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      Stage64& T = g ? T1 : T0;
+#pragma unroll
+      for (int o = 0; o < PA; o++) dm.op_a(o, lds_addr(T.a), g);
+#pragma unroll
+      for (int o = 0; o < PB; o++) dm.op_b(o, lds_addr(T.b), g);
+    }
+  } else {
+    const uint32_t l0 = lds_addr(L);
+#pragma unroll
+    for (int o = 0; o < PB; o++) dm.op_b(o, l0 + 3 * SA * 16, 0);
+#pragma unroll
+    for (int o = 0; o < PA; o++) dm.op_a(o, l0, 0);
+#pragma unroll
+    for (int o = 0; o < PB; o++) dm.op_b(o, l0 + (3 * SA + SW) * 16, 1);
+#pragma unroll
+    for (int o = 0; o < PA; o++) dm.op_a(o, l0 + SA * 16, 1);
+#pragma unroll
+    for (int o = 0; o < PA; o++) dm.op_a(o, l0 + 2 * SA * 16, 2);
+  }
 
   // Output coordinates.  Transposed product: lane holds, for block (i, j) and element e, output row
   // rbase + 32 i + lane % 32 and columns cbase + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4, i.e. four
@@ -571,8 +668,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
   const int arow = wm * WTM + l32, brow = wn * WTN + l32;
   const int sw = (lane & 7) ^ ((lane >> 3) & 1);          // g(row) of fragment rows 32 n + lane % 32
-  if (swap) xl_k_loop64<true>(acc, T0, T1, dm, arow, brow, hi, sw);
-  else xl_k_loop64<false>(acc, T0, T1, dm, arow, brow, hi, sw);
+  if constexpr (RING) {
+    if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
+    else xl_k_loop64r<false, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
+  } else {
+    if (swap) xl_k_loop64<true>(acc, T0, T1, dm, arow, brow, hi, sw);
+    else xl_k_loop64<false>(acc, T0, T1, dm, arow, brow, hi, sw);
+  }
 
   // ---------------- epilogue ----------------
   // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
@@ -582,8 +684,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // All global loads are issued before the first store: on gfx9 vmcnt counts stores too, so a load
   // issued after a store would wait for it.
   __syncthreads();                                        // every wave is done with the K stages
-  constexpr int SB = (int)(sizeof(Stage) / 4);             // staging bytes per wave
-  char* stg = reinterpret_cast<char*>(&S4) + wave * SB;
+  char* stg = reinterpret_cast<char*>(L) + wave * SB;
   auto sync_wave = [] {                                   // this wave's LDS writes are visible to it
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
@@ -703,8 +804,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       constexpr int CW = fitw(WTN, SB / 64), CPR = CW / 8;
       static_assert(CW % 64 == 0, "whole heads per staged block");
       const bool rope = a.rope_cos != nullptr;
-      float* tcos = reinterpret_cast<float*>(&T0);
-      float* tsin = reinterpret_cast<float*>(&T1);
+      float* tcos = reinterpret_cast<float*>(reinterpret_cast<char*>(L) + 4 * SB);
+      float* tsin = tcos + BM * 32;
       if (rope) {
         // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
         // four 16-byte pieces per thread at a time (the positions were loaded before the K loop)
@@ -804,11 +905,36 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
 // GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
 // build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
+// compute units of the current device, cached per device (256 if the query fails: the count only
+// picks between two K loops that give the same bits)
+static int num_cus() {
+  static std::atomic<int> cached[16];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool RING>
+static void launch_xl_ring(const GemmArgs& a, int tiles, hipStream_t st) {
+  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, RING>), dim3(tiles), dim3(256), 0, st, a);
+  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, RING>), dim3(tiles), dim3(256), 0, st, a);
+}
+
+// 128x128 tiles take the three-A-buffer loop when the grid has more tiles than the chip has CUs,
+// i.e. when CUs run two workgroups whose stages interleave; with one workgroup per CU the
+// two-buffer loop is faster.  Both give the same bits.
 template <int BM, int BN, int WM, int WN, int EPI, int ACT>
 static void launch_xl_hb(const GemmArgs& a, hipStream_t st) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (EPI == EPI_PARTIAL ? a.ksplit : 1);
-  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true>), dim3(tiles), dim3(256), 0, st, a);
-  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false>), dim3(tiles), dim3(256), 0, st, a);
+  if constexpr (BM * BN <= 128 * 128) {
+    if (tiles > num_cus()) { launch_xl_ring<BM, BN, WM, WN, EPI, ACT, true>(a, tiles, st); return; }
+  }
+  launch_xl_ring<BM, BN, WM, WN, EPI, ACT, false>(a, tiles, st);
 }
 
 template <int BM, int BN, int WM, int WN>
