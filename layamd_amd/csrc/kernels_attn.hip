@@ -340,6 +340,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 
   fetch_k(lo, Ks0);
   fetch_v(lo);
+  // The Q fragments must be in registers before the key loop, and the compiler must know it.  Left
+  // to itself it sinks their loads to the loop entry, and its wait analysis then counts them as
+  // outstanding in every iteration: vmcnt(3..0) before the Q K^T MFMAs, which in later iterations
+  // wait for the next block's K fetch issued just before them.  Using the registers here makes it
+  // wait for the loads once, before the loop.
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");

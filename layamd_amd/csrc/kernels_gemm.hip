@@ -640,8 +640,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   if constexpr (EPI == EPI_RESID) {
     // the residual update X += A W^T + b starts the accumulators at X (16-byte loads of 4 columns;
     // rows past M read 0, columns past N are never stored), so the epilogue loads nothing after its
-    // first store.  These loads come after the DMA fills, so the wait for them (before the first
-    // MFMA) also covers the prologue slices.
+    // first store.  These loads come after the DMA fills, so the wait for them (before the K loop)
+    // also covers the prologue stages.
     const __amdgpu_buffer_rsrc_t rX =
         __builtin_amdgcn_make_buffer_rsrc(a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
 #pragma unroll
@@ -657,6 +657,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
           for (int u = 0; u < 4; u++) acc[i][j][4 * g + u] = x[u];
         }
+    // Wait for these loads once, here, with a wait the compiler sees (not inline assembly).  Left to
+    // itself it places the waits at the MFMAs inside the K loop and, since its wait analysis merges
+    // the loop entry into every iteration, repeats them there: vmcnt(44..0) at the top of each
+    // iteration, which after the first one wait for the next stage's DMA fills instead.
+    __builtin_amdgcn_s_waitcnt(0x0F70);                   // vmcnt(0); expcnt, lgkmcnt: no wait
   } else {
 #pragma unroll
     for (int i = 0; i < FM; i++)
