@@ -138,8 +138,8 @@ def main():
            "LAYA_PROFILE": None}
     if a.pmc_probe:
         # counter runs serialize every dispatch, so tile timing is meaningless there: pin the plan the
-        # tuner picks for the dominant stage at this workload (256x256 over 9216 rows, 128x128 after)
-        env.update({"LAYA_GEMM_CFG": 0, "LAYA_GEMM_SPLIT": "9216,3"})
+        # tuner picks for the dominant stage at this workload (128x128 tiles, one launch)
+        env.update({"LAYA_GEMM_CFG": 3})
     eng = le.Engine(None, mdir, precision=precision, env=env)
     flat = batch.flat()
     if a.pmc_probe:
