@@ -910,15 +910,23 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
 // GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
 // build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
-// compute units of the current device, cached per device (256 if the query fails: the count only
-// picks between two K loops that give the same bits)
+// compute units of the current device, cached per device.  If the query fails (a process whose
+// HIP runtime instance has no current device, e.g. a host that drives the library through streams
+// of another runtime), the count is 256 and the query's error is cleared so that the caller's
+// error check does not see it: the count only picks between two K loops that give the same bits.
 static int num_cus() {
   static std::atomic<int> cached[16];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) {
+    (void)hipGetLastError();
+    return 256;
+  }
   int n = cached[dev].load(std::memory_order_relaxed);
   if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
     cached[dev].store(n, std::memory_order_relaxed);
   }
   return n;

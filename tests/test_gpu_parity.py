@@ -92,6 +92,54 @@ def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
         le.gemm_config(lib, prev)
 
 
+# 128x128 tiles run the three-A-buffer K loop when the grid has more tiles than the chip has CUs
+# (two workgroups per CU), the two-buffer loop otherwise
+def _ring_rows(n_tiles_per_row):
+    import torch
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    return 128 * (ncu // n_tiles_per_row + 1), 128 * max(1, ncu // (2 * n_tiles_per_row))
+
+
+@pytest.mark.parametrize("N,K", [(1024, 512), (2048, 2624)])
+def test_gemm_ring_vs_torch(N, K):
+    lib = le.load_library()
+    M, _ = _ring_rows(N // 128)
+    prev = le.gemm_config(lib, 3)
+    try:
+        _check_gemm(lib, "bf16", M, N, K)
+    finally:
+        le.gemm_config(lib, prev)
+
+
+def test_gemm_ring_bit_identical_to_two_buffer_loop():
+    """The first rows of a GEMM give the same bits through the ring loop (a grid of more 128x128
+    tiles than CUs) and through the two-buffer loop (the same rows alone, a grid of fewer), for a
+    GELU store and a residual update."""
+    import torch
+    lib = le.load_library()
+    N, K = 1024, 2624
+    M, part = _ring_rows(N // 128)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    X0 = torch.randn(M, N, generator=g).float().cuda()
+    prev = le.gemm_config(lib, 3)
+    try:
+        C1 = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+        le.gemm(lib, A, W, C1, act=2)
+        C2 = torch.zeros(part, N, dtype=torch.bfloat16, device="cuda")
+        le.gemm(lib, A[:part].contiguous(), W, C2, act=2)
+        X1 = X0.clone()
+        le.gemm(lib, A, W, X1, residual=True)
+        X2 = X0[:part].clone()
+        le.gemm(lib, A[:part].contiguous(), W, X2, residual=True)
+        torch.cuda.synchronize()
+    finally:
+        le.gemm_config(lib, prev)
+    assert torch.equal(C1[:part].cpu(), C2.cpu())
+    assert torch.equal(X1[:part].cpu(), X2.cpu())
+
+
 # split-K: K in ks chunks of fp32 partial products, summed in chunk order (bf16 operands)
 @pytest.mark.parametrize("ks", [2, 4, 8, 16])
 @pytest.mark.parametrize("M,N,K", [(160, 1024, 1024), (300, 384, 1024), (1, 256, 4096), (1300, 512, 2048)])
