@@ -453,7 +453,7 @@ struct Engine : EngineIface {
     std::vector<TilePlan> cands = {first};
     for (int c = 0; c < kGemmConfigs; c++)
       if (c != first.cfg && gemm_config_valid(epi, g, c)) cands.push_back(TilePlan{c, 0, -1});
-    for (int c1 : {0, 4}) {
+    for (int c1 : {0, 4, 5}) {
       if (!gemm_config_valid(epi, g, c1)) continue;
       const int bm = gemm_config_bm(c1), tn = (g.N + gemm_config_bn(c1) - 1) / gemm_config_bn(c1);
       const int rounds = ((g.M + bm - 1) / bm) * tn / n_cu;

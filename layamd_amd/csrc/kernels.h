@@ -57,8 +57,8 @@ struct GemmArgs {
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
-// pins the bf16 tile configuration for later launches (-1: the planner; 0..4: 256x256, 256x128,
-// 128x256, 128x128, 192x256); returns the previous setting
+// pins the bf16 tile configuration for later launches (-1: the planner; 0..5: 256x256, 256x128,
+// 128x256, 128x128, 192x256, 160x256); returns the previous setting
 int gemm_config(int cfg);
 int gemm_pinned();                               // the pinned configuration, or -1
 // row split used together with the pinned configuration: rows [split_rows, M) run as a second
@@ -67,7 +67,7 @@ void gemm_pin_split(int split_rows, int cfg_tail);
 // split-K factor applied to later bf16 EPI_STORE / EPI_RESID launches that name none (<= 1: none);
 // returns the previous one
 int gemm_pin_ksplit(int ks);
-constexpr int kGemmConfigs = 5;
+constexpr int kGemmConfigs = 6;
 // whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
 // shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)
 bool gemm_config_valid(int epi, const GemmArgs& a, int cfg);

@@ -549,7 +549,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   constexpr int BMQ = (BM + 31) / 32 * 32;
   constexpr int PA = BMQ / 32, PB = BN / 32;             // DMA instructions per wave and stage
   static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0 && BN % 64 == 0, "tile");
-  static_assert(PA % 2 == 0 && PB % 2 == 0, "swizzle parity: even instruction count per wave");
+  static_assert(PB % 2 == 0, "swizzle parity of the W part: even instruction count per wave");
   // K stages: two whole stages (A then W part), or (RING) three A buffers and two W buffers (BMQ and
   // BN rows of 128 bytes); after the K loop the same memory holds the epilogue's staging area (SB
   // bytes per wave) and, for the QKV projection, the RoPE tables of the tile's rows
@@ -597,8 +597,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   dm.rB = make_rsrc(reinterpret_cast<const T*>(a.W) + k0, (uint32_t)(((size_t)a.N * a.ldw - k0) * sizeof(T)));
   dm.rNone = make_rsrc(a.A, 0u);           // zero length: every offset out of range
   const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
-  dm.va[0] = dma64_voff(m0, wave * PA * 8, lda_b, lane, 0);
-  dm.va[1] = dma64_voff(m0, wave * PA * 8, lda_b, lane, 1);
+  // instruction o of this wave fills rows 8 (wave PA + o) ..: the swizzle's row term is the parity
+  // of wave PA + o (PA may be odd)
+  dm.va[0] = dma64_voff(m0, wave * PA * 8, lda_b, lane, (wave * PA) & 1);
+  dm.va[1] = dma64_voff(m0, wave * PA * 8, lda_b, lane, ((wave * PA) & 1) ^ 1);
   dm.vb[0] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 0);
   dm.vb[1] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 1);
   dm.wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
@@ -980,7 +982,7 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
 // BM <= BN.
 struct XlCfg { int bm, bn, per_cu; float rel; };
 static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80f}, {128, 256, 1, 0.83f},
-                                        {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}};
+                                        {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}, {160, 256, 1, 0.93f}};
 
 // tile configuration pinned for every bf16 launch (-1: none); LAYA_GEMM_CFG sets it at the first
 // launch, gemm_config() at run time
@@ -1109,6 +1111,7 @@ static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
     case 2: launch_xl<128, 256, 2, 2>(epi, a, st); return;
     case 3: launch_xl<128, 128, 2, 2>(epi, a, st); return;
     case 4: launch_xl<192, 256, 2, 2>(epi, a, st); return;
+    case 5: launch_xl<160, 256, 1, 4>(epi, a, st); return;
     default: fprintf(stderr, "[laya] gemm: bad tile configuration %d\n", cfg); exit(1);
   }
 }

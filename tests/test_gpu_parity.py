@@ -65,7 +65,7 @@ def golden_flat_logits(c):
 
 # ---------------------------------------------------------------- GEMM kernel vs torch fp32
 # bf16 runs every tile configuration of the MFMA GEMM (-1: the planner's choice)
-@pytest.mark.parametrize("dtype,cfg", [("fp32", -1)] + [("bf16", c) for c in (-1, 0, 1, 2, 3, 4)])
+@pytest.mark.parametrize("dtype,cfg", [("fp32", -1)] + [("bf16", c) for c in (-1, 0, 1, 2, 3, 4, 5)])
 @pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (200, 256, 320),
                                    (513, 1024, 2624)])
 def test_gemm_vs_torch(dtype, cfg, M, N, K):
@@ -79,7 +79,7 @@ def test_gemm_vs_torch(dtype, cfg, M, N, K):
 
 
 # row splits: rows [split, M) in a second launch with another tile shape (split >= M: one launch)
-@pytest.mark.parametrize("cfg,split,tail", [(0, 256, 3), (4, 192, 2), (3, 128, 1), (0, 264, 4)])
+@pytest.mark.parametrize("cfg,split,tail", [(0, 256, 3), (4, 192, 2), (3, 128, 1), (0, 264, 4), (5, 160, 3)])
 @pytest.mark.parametrize("M,N,K", [(300, 384, 192), (513, 1024, 2624), (200, 256, 320)])
 def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
     lib = le.load_library()
@@ -390,7 +390,7 @@ def test_tile_configs_bit_identical():
     prev = le.gemm_config(e.lib, -1)
     try:
         ref_lo, ref_ac = e.forward_flat(*b.flat())
-        for cfg in (0, 1, 2, 3, 4):
+        for cfg in (0, 1, 2, 3, 4, 5):
             le.gemm_config(e.lib, cfg)
             lo, ac = e.forward_flat(*b.flat())
             assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
