@@ -230,8 +230,9 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 //   O^T[d][query] += V^T P^T  A = V^T rows (32 d x 16 keys),       B = P^T from the S^T registers
 //
 // The 32x32 accumulator gives lane l query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of a
-// 32-key sub-block, so lanes l and l ^ 32 together hold a query's 64 scores: row max and row sum
-// take one cross-lane step.  Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand
+// 32-key sub-block, so lanes l and l ^ 32 together hold a query's 64 scores: the row max takes one
+// cross-lane step, and the row sum is one more MFMA per PV step (an all-ones A operand times P^T).
+// Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand
 // of one 16-key PV step with k-index i <-> key 16 h' + 8 (i / 4) + 4 (l / 32) + i % 4; the V^T
 // operand reads the same keys (two 8-byte pieces per lane).  Scores are scaled into the log2
 // domain once (exp2); blocks whose keys are all visible to every query of the tile skip the mask.
@@ -328,14 +329,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     for (int j = 0; j < 4; j++) attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
   };
 
-  f32x16_t o[2];
+  f32x16_t o[2], lsum;
 #pragma unroll
-  for (int db = 0; db < 2; db++)
-#pragma unroll
-    for (int e = 0; e < 16; e++) o[db][e] = 0.f;
-  // running max of the raw scores (scale > 0 keeps the order) and running sum; probabilities are
-  // exp2(s * c - m * c) with c = scale * log2(e), one FMA per score
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int e = 0; e < 16; e++) {
+    o[0][e] = 0.f;
+    o[1][e] = 0.f;
+    lsum[e] = 0.f;
+  }
+  // running max of the raw scores (scale > 0 keeps the order); probabilities are
+  // exp2(s * c - m * c) with c = scale * log2(e), one FMA per score.  The running sum of the
+  // probabilities is an MFMA of an all-ones A operand with P^T (the MFMA pipe has room, the VALU
+  // has none): every element of lsum holds the sum over the keys so far of this lane's query, summed
+  // over exactly the bf16 values that the PV product uses.
+  float m_run = -INFINITY;
+  const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
   const float c2 = scale * 1.44269504088896340736f;
 
   fetch_k(lo, Ks0);
@@ -397,23 +404,17 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     const float m_new = fmaxf(m_run, mx);
     // with no visible key yet (m_new = -inf) every exp2 below is exp2(-inf) = 0
     const float mc = m_new == -INFINITY ? 0.f : m_new * c2;
-    float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        st[kb][e] = __builtin_amdgcn_exp2f(fmaf(st[kb][e], c2, -mc));
-        rs += st[kb][e];
-      }
-    rs += __shfl_xor(rs, 32, 64);
-    // the running output is rescaled only when some lane's max moved (alpha == 1 otherwise)
+      for (int e = 0; e < 16; e++) st[kb][e] = __builtin_amdgcn_exp2f(fmaf(st[kb][e], c2, -mc));
+    // the running output and sum are rescaled only when some lane's max moved (alpha == 1 otherwise)
     if (__any(m_new != m_run)) {
       const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, -mc));
-      l_run *= alpha;
+      lsum *= alpha;
 #pragma unroll
       for (int db = 0; db < 2; db++) o[db] *= alpha;
     }
-    l_run += rs;
     m_run = m_new;
 
     // this block's V^T (fetched after the previous PV step, before the K fetch above) has landed
@@ -441,6 +442,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
         const u32x4_t va = (u32x4_t){u0.x, u0.y, u1.x, u1.y};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pb, o[db], 0, 0, 0);
       }
+      lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb, lsum, 0, 0, 0);
     }
     // the next block's K has landed (this wave's part) and no wave still reads V^T or this K
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -451,6 +453,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 
   if (!qvalid) return;
   // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4
+  const float l_run = lsum[0];
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   bf16_t* orow_p = O + (size_t)orow * ldo + h * HD;
 #pragma unroll
