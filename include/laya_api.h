@@ -54,8 +54,9 @@ void laya_prof_report(void* h, int iters);
 /* Clears the per-stage table.  Replaces src/engine.hip:557. */
 void laya_prof_reset(void* h);
 
-/* Warm-up.  The MI355X engine has fixed tile configurations and no library autotuning, so this
- * only loads every kernel once.  Replaces src/engine.hip:558 (laya_tune_all). */
+/* GEMM tuning ahead of traffic: times the engine's tile configurations for every GEMM of every
+ * row bucket up to the pass capacity (otherwise each new pass shape is timed before its first
+ * run).  Replaces src/engine.hip:558 (laya_tune_all, which times hipBLASLt plans per bucket). */
 void laya_tune_all(void* h);
 
 #ifdef __cplusplus
