@@ -190,6 +190,24 @@ def main():
     eng.prof_report(n_prof)
     sys.stdout.flush()
 
+    # achievable peaks on this box, outside the timed region: a register-only MFMA loop on every
+    # CU (the clock the chip holds under MFMA load) and a device-to-device copy of 1 GiB
+    mfma_ach = le.mfma_peak(eng.lib)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2.0 * (1 << 30) * 5 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+    del src, dst
+    achievable = {"mfma_bf16_tflops": round(mfma_ach, 1), "hbm_copy_gbs": round(copy_gbs, 1),
+                  "method": "register-only v_mfma_f32_32x32x16_bf16 loop, 2 workgroups of 4 waves per CU "
+                            "(laya_ext_mfma_loop); torch device-to-device copy of 1 GiB, read + write bytes"}
+
     T, B, KT = batch.tokens, batch.B, int(batch.nmark.sum())
     R = KT + B
     af = attention_flops(batch.lens, cfg.d, cfg.local_attention // 2)
@@ -204,12 +222,15 @@ def main():
             if fl and "gemm" in name:
                 entry["tflops"] = round(fl / (avg_ms * 1e-3) / 1e12, 1)
                 entry["frac_mfma"] = round(fl / (avg_ms * 1e-3) / (PEAK_BF16 if elt == 2 else PEAK_FP32), 4)
+                if elt == 2:
+                    entry["frac_achievable_mfma"] = round(fl / (avg_ms * 1e-3) / 1e12 / mfma_ach, 4)
                 if name.startswith("enc:"):
                     gemm_flops += fl * calls
                     gemm_ms += ms
             else:
                 entry["gbs"] = round(by / (avg_ms * 1e-3) / 1e9, 1)
                 entry["frac_hbm"] = round(by / (avg_ms * 1e-3) / PEAK_HBM, 4)
+                entry["frac_achievable_hbm"] = round(by / (avg_ms * 1e-3) / 1e9 / copy_gbs, 4)
                 if fl:
                     entry["tflops"] = round(fl / (avg_ms * 1e-3) / 1e12, 1)
         kernels[name] = entry
@@ -221,11 +242,13 @@ def main():
         peak = (PEAK_BF16 if elt == 2 else PEAK_FP32) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(ach / peak, 4), "traffic": measured_traffic(dom), "kernel": dom,
-                "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T)}
+                "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T),
+                "achievable_peak": round(mfma_ach, 1), "frac_of_achievable": round(ach / mfma_ach, 4)}
     else:
         ach = by / (dom_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "kernel": dom}
+                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "kernel": dom,
+                "achievable_peak": round(copy_gbs, 1), "frac_of_achievable": round(ach / copy_gbs, 4)}
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -247,6 +270,7 @@ def main():
         if gemm_ms else None,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "achievable": achievable,
         "kernels": kernels,
     }
     print(json.dumps(line))

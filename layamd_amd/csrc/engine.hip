@@ -771,6 +771,28 @@ int laya_ext_replay(void* h, int iters, float* ms) { return E(h)->replay(iters, 
 static float* g_ext_ws = nullptr;          // split-K workspace of laya_ext_gemm (caller's memory)
 static size_t g_ext_ws_bytes = 0;
 
+int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, float* ms, double* flops) {
+  using namespace laya;
+  if (!out || blocks < 1 || iters < 1) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  hipEvent_t a, b;
+  LAYA_HIP(hipEventCreate(&a));
+  LAYA_HIP(hipEventCreate(&b));
+  launch_mfma_loop(out, blocks, iters, st);              // warm-up: the clock settles under load
+  LAYA_HIP(hipEventRecord(a, st));
+  launch_mfma_loop(out, blocks, iters, st);
+  LAYA_HIP(hipEventRecord(b, st));
+  LAYA_HIP(hipEventSynchronize(b));
+  float t = 0.f;
+  LAYA_HIP(hipEventElapsedTime(&t, a, b));
+  LAYA_HIP(hipEventDestroy(a));
+  LAYA_HIP(hipEventDestroy(b));
+  LAYA_HIP(hipGetLastError());
+  if (ms) *ms = t;
+  if (flops) *flops = (double)blocks * 4.0 * iters * 8.0 * 32768.0;
+  return 0;
+}
+
 int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
                   int K, void* stream, int iters, float* ms) {
   using namespace laya;

@@ -68,6 +68,9 @@ void gemm_pin_split(int split_rows, int cfg_tail);
 // returns the previous one
 int gemm_pin_ksplit(int ks);
 constexpr int kGemmConfigs = 6;
+// the achievable-MFMA probe: blocks x 4 waves, each iters x 8 MFMAs of 32x32x16 bf16 (32768 flop);
+// out holds blocks x 256 floats
+void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st);
 // whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
 // shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)
 bool gemm_config_valid(int epi, const GemmArgs& a, int cfg);

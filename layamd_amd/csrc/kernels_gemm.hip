@@ -912,6 +912,37 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
 // GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
 // build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
+// The achievable bf16 MFMA rate of the chip at the clock it holds under MFMA load: every wave
+// issues v_mfma_f32_32x32x16_bf16 back to back on eight independent register accumulators, with
+// no memory traffic, and stores one value per lane at the end (so the work is kept).  32768 flop
+// per MFMA; blocks of 4 waves.
+__global__ __launch_bounds__(256) void k_mfma_loop(float* __restrict__ out, int iters) {
+  f32x16_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
+  bf16x8_t a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (__bf16)(1e-3f * (float)((threadIdx.x + i) & 7));
+    b[i] = (__bf16)(1e-3f * (float)((threadIdx.x * 3 + i) & 7));
+  }
+  for (int it = 0; it < iters; it++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) s += acc[j][e];
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st) {
+  hipLaunchKernelGGL(k_mfma_loop, dim3(blocks), dim3(256), 0, st, out, iters);
+}
+
 // compute units of the current device, cached per device.  If the query fails (a process whose
 // HIP runtime instance has no current device, e.g. a host that drives the library through streams
 // of another runtime), the count is 256 and the query's error is cleared so that the caller's

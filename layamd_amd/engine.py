@@ -25,7 +25,7 @@ HOST_LIB = os.path.join(PKG, "liblaya_host.so")
 ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act", "laya_max_len",
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
-               "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit"]
+               "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop"]
 
 _IP = ctypes.POINTER(ctypes.c_int)
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -77,6 +77,9 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_gemm_split.restype = ctypes.c_int
     L.laya_ext_gemm_ksplit.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
     L.laya_ext_gemm_ksplit.restype = ctypes.c_int
+    L.laya_ext_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, _FP,
+                                     ctypes.POINTER(ctypes.c_double)]
+    L.laya_ext_mfma_loop.restype = ctypes.c_int
     return L
 
 
@@ -106,6 +109,21 @@ def gemm_split(lib, split_rows: int, cfg_tail: int = -1):
     """Row split for pinned bf16 launches: rows [split_rows, M) in a second launch with cfg_tail."""
     if lib.laya_ext_gemm_split(split_rows, cfg_tail) != 0:
         raise ValueError("invalid GEMM split %d / %d" % (split_rows, cfg_tail))
+
+
+def mfma_peak(lib, blocks_per_cu: int = 2, iters: int = 4096) -> float:
+    """The chip's achievable bf16 MFMA rate in TFLOP/s (register-only MFMA loop on every CU)."""
+    import torch
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = ncu * blocks_per_cu
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    ms, flops = ctypes.c_float(), ctypes.c_double()
+    rc = lib.laya_ext_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters,
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.byref(ms),
+                                ctypes.byref(flops))
+    if rc != 0:
+        raise RuntimeError("mfma loop rejected")
+    return flops.value / (ms.value * 1e-3) / 1e12
 
 
 def gemm_ksplit(lib, ks: int, ws=None) -> int:
