@@ -272,6 +272,23 @@ def test_packing_and_permutation_invariance(precision):
         o += nm[i]
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_tiny_extremes_vs_oracle(precision):
+    """The limits of the interface against the CPU oracle: a question of the maximum length (320),
+    one with the maximum of 255 markers, single-token and single-marker questions, in one call."""
+    from oracle import model as om
+    cfg, W = ck.load_checkpoint(checkpoint_dir("tiny"))
+    b = wl.make_batch(ck.PRESETS["tiny"], [5, 64, 65, 130, 1, 320, 300], [2, 3, 1, 12, 1, 4, 255], seed=3)
+    lo, ac = engine("tiny", precision).forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["tiny"], b)
+    d = prob_delta(lo, ref_lo, b.nmark)
+    da = float((np.abs(ac - ref_ac) / np.maximum(1.0, np.abs(ref_ac))).max())
+    if precision == "fp32":
+        assert np.abs(lo - ref_lo).max() < 1e-4 and d < FP32_PROB and da < FP32_ACT, (d, da)
+    else:
+        assert d < BF16_PROB, d
+
+
 def test_graph_replay_matches_eager():
     e = engine("tiny", "bf16")
     b1 = wl.make_batch(ck.PRESETS["tiny"], [40, 200, 17], [3, 2, 5], seed=11)
