@@ -140,6 +140,14 @@ def test_gemm_ring_bit_identical_to_two_buffer_loop():
     assert torch.equal(X1[:part].cpu(), X2.cpu())
 
 
+def test_mfma_loop_probe():
+    """The achievable-peak probe runs and reports a rate between a tenth of the published bf16
+    peak and the peak itself (the chip cannot beat 2.5166 PF; a broken probe reads far lower)."""
+    lib = le.load_library()
+    tf = le.mfma_peak(lib, blocks_per_cu=2, iters=1024)
+    assert 251.0 < tf < 2517.0, tf
+
+
 # split-K: K in ks chunks of fp32 partial products, summed in chunk order (bf16 operands)
 @pytest.mark.parametrize("ks", [2, 4, 8, 16])
 @pytest.mark.parametrize("M,N,K", [(160, 1024, 1024), (300, 384, 1024), (1, 256, 4096), (1300, 512, 2048)])
