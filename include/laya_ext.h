@@ -36,12 +36,12 @@ const char* laya_ext_precision(void* h);
 int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
                   int K, void* stream, int iters, float* ms);
 
-/* The chip's achievable bf16 MFMA rate: blocks of 4 waves, each issuing iters x 8 independent
- * v_mfma_f32_32x32x16_bf16 on registers (no memory traffic), on stream; out is the caller's device
- * buffer of blocks x 256 floats.  One warm-up launch, then one timed launch: *ms gets its time and
- * *flops its work.  No counterpart in the reference: it gives bench.py the achievable peak next to
- * the published one.  Returns 0, or -1 for invalid arguments. */
-int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, float* ms, double* flops);
+/* The chip's achievable bf16 MFMA rate: launches (does not wait for) blocks of 4 waves on stream,
+ * each issuing iters x 8 independent v_mfma_f32_32x32x16_bf16 on registers (no memory traffic);
+ * out is the caller's device buffer of blocks x 256 floats, *flops gets the launch's work.  The
+ * caller times it with its own events.  No counterpart in the reference: it gives bench.py the
+ * achievable peak next to the published one.  Returns 0, or -1 for invalid arguments. */
+int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* flops);
 
 /* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 lets the planner
  * choose per GEMM (the default, or LAYA_GEMM_CFG); 0..5 select 256x256, 256x128, 128x256, 128x128,

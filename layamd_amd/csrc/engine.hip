@@ -771,24 +771,17 @@ int laya_ext_replay(void* h, int iters, float* ms) { return E(h)->replay(iters, 
 static float* g_ext_ws = nullptr;          // split-K workspace of laya_ext_gemm (caller's memory)
 static size_t g_ext_ws_bytes = 0;
 
-int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, float* ms, double* flops) {
+// The measurement hooks run inside the caller's process, which shares the HIP runtime (and its
+// per-thread last error) with the caller: a stale error that the caller's own HIP calls left must
+// not be reported as this launch's, so each hook clears it first and then checks its own launches.
+
+// launch only: the caller times it with its own events on its stream
+int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* flops) {
   using namespace laya;
   if (!out || blocks < 1 || iters < 1) return -1;
-  hipStream_t st = (hipStream_t)stream;
-  hipEvent_t a, b;
-  LAYA_HIP(hipEventCreate(&a));
-  LAYA_HIP(hipEventCreate(&b));
-  launch_mfma_loop(out, blocks, iters, st);              // warm-up: the clock settles under load
-  LAYA_HIP(hipEventRecord(a, st));
-  launch_mfma_loop(out, blocks, iters, st);
-  LAYA_HIP(hipEventRecord(b, st));
-  LAYA_HIP(hipEventSynchronize(b));
-  float t = 0.f;
-  LAYA_HIP(hipEventElapsedTime(&t, a, b));
-  LAYA_HIP(hipEventDestroy(a));
-  LAYA_HIP(hipEventDestroy(b));
+  (void)hipGetLastError();
+  launch_mfma_loop(out, blocks, iters, (hipStream_t)stream);
   LAYA_HIP(hipGetLastError());
-  if (ms) *ms = t;
   if (flops) *flops = (double)blocks * 4.0 * iters * 8.0 * 32768.0;
   return 0;
 }
@@ -803,6 +796,7 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
   const char* why = "";
   if (!gemm_shape_ok(epi == 0 ? EPI_STORE : EPI_RESID, g, dtype == 0 ? 4 : 2, &why)) return -1;
   hipStream_t st = (hipStream_t)stream;
+  (void)hipGetLastError();
   // a pinned split-K factor runs in the caller's workspace (laya_ext_gemm_ksplit)
   g.ws = g_ext_ws;
   g.ws_bytes = g_ext_ws_bytes;

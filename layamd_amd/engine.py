@@ -11,8 +11,10 @@ The library is the in-tree build (layamd_amd/liblaya.so, or $LAYA_LIB).  There i
 a missing library raises.
 """
 import ctypes
+import importlib.util
 import itertools
 import os
+import sys
 from array import array
 from typing import List, Optional
 
@@ -36,10 +38,17 @@ def lib_path() -> str:
 
 
 def load_library(path: Optional[str] = None) -> ctypes.CDLL:
-    """Loads liblaya.so and declares every exported signature (no GPU work happens here)."""
+    """Loads liblaya.so and declares every exported signature (no GPU work happens here).
+
+    When PyTorch is installed it is imported first.  Both name the same HIP runtime library
+    (SONAME libamdhip64.so.7), so liblaya.so then binds to the runtime instance torch loaded and
+    the two share the device, streams and memory.  Loaded the other way round, torch brings a second
+    instance of the runtime, and the library's instance sees no device."""
     path = path or lib_path()
     if not os.path.exists(path):
         raise FileNotFoundError("liblaya.so not built at %s (run python -m layamd_amd.build)" % path)
+    if "torch" not in sys.modules and importlib.util.find_spec("torch") is not None:
+        import torch  # noqa: F401
     L = ctypes.CDLL(path)
     L.laya_create.restype = ctypes.c_void_p
     L.laya_create.argtypes = [ctypes.c_char_p]
@@ -77,7 +86,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_gemm_split.restype = ctypes.c_int
     L.laya_ext_gemm_ksplit.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
     L.laya_ext_gemm_ksplit.restype = ctypes.c_int
-    L.laya_ext_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, _FP,
+    L.laya_ext_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.POINTER(ctypes.c_double)]
     L.laya_ext_mfma_loop.restype = ctypes.c_int
     return L
@@ -117,13 +126,20 @@ def mfma_peak(lib, blocks_per_cu: int = 2, iters: int = 4096) -> float:
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     blocks = ncu * blocks_per_cu
     out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
-    ms, flops = ctypes.c_float(), ctypes.c_double()
-    rc = lib.laya_ext_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters,
-                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.byref(ms),
-                                ctypes.byref(flops))
-    if rc != 0:
-        raise RuntimeError("mfma loop rejected")
-    return flops.value / (ms.value * 1e-3) / 1e12
+    flops = ctypes.c_double()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch():
+        if lib.laya_ext_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters, st, ctypes.byref(flops)) != 0:
+            raise RuntimeError("mfma loop rejected")
+
+    launch()                                             # warm-up: the clock settles under load
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    launch()
+    b.record()
+    torch.cuda.synchronize()
+    return flops.value / (a.elapsed_time(b) * 1e-3) / 1e12
 
 
 def gemm_ksplit(lib, ks: int, ws=None) -> int:
