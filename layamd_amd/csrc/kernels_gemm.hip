@@ -1014,7 +1014,7 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
 struct XlCfg { int bm, bn, per_cu; float rel; };
 static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80f}, {128, 256, 1, 0.83f},
                                         {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}, {160, 256, 1, 0.93f},
-                                        {128, 192, 2, 0.80f}};
+                                        {128, 192, 2, 0.80f}, {192, 128, 2, 0.80f}};
 
 // tile configuration pinned for every bf16 launch (-1: none); LAYA_GEMM_CFG sets it at the first
 // launch, gemm_config() at run time
@@ -1145,6 +1145,7 @@ static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
     case 4: launch_xl<192, 256, 2, 2>(epi, a, st); return;
     case 5: launch_xl<160, 256, 1, 4>(epi, a, st); return;
     case 6: launch_xl<128, 192, 4, 1>(epi, a, st); return;
+    case 7: launch_xl<192, 128, 2, 2>(epi, a, st); return;
     default: fprintf(stderr, "[laya] gemm: bad tile configuration %d\n", cfg); exit(1);
   }
 }
