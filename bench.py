@@ -138,8 +138,8 @@ def main():
            "LAYA_PROFILE": None}
     if a.pmc_probe:
         # counter runs serialize every dispatch, so tile timing is meaningless there: pin the plan the
-        # tuner picks for the dominant stage at this workload (128x128 tiles, one launch)
-        env.update({"LAYA_GEMM_CFG": 3})
+        # tuner picks for the dominant stage at this workload (192x128 tiles, one launch)
+        env.update({"LAYA_GEMM_CFG": 7})
     eng = le.Engine(None, mdir, precision=precision, env=env)
     flat = batch.flat()
     if a.pmc_probe:
