@@ -4,13 +4,88 @@ runs (rocprofv3 --pmc) of a single kernel:
     python -m layamd_amd.gemm_probe --M 16384 --N 4096 --K 4096 --cfg 0 --iters 4
 
 A = N(0,1) and W = N(0,0.02) in bf16, C = A W^T stored in bf16 (plain epilogue, no bias).  --cfg
-pins the tile configuration (0..5, see include/laya_ext.h; -1: the planner).  Prints the time per
+pins the tile configuration (0..7, see include/laya_ext.h; -1: the planner).  Prints the time per
 launch and the TFLOP/s on 2 M N K flop.
+
+    python -m layamd_amd.gemm_probe --c2
+
+times the GEMM microbenchmark shapes instead: M in {512, 16384}, (N, K) in {(3072, 1024),
+(1024, 1024), (5248, 1024), (1024, 2624)}, bf16 and fp32 operands, against torch.mm (hipBLASLt or
+rocBLAS) on the same device.  bf16 tries the planner and every tile configuration (with split-K
+factors 2, 4 and 8 at M = 512 where K allows them) and reports the best; each engine result is checked
+against torch.mm.  Prints a markdown table.
 """
 import argparse
 import time
 
 from layamd_amd import engine as le
+
+
+C2_SHAPES = [(M, N, K) for M in (512, 16384) for (N, K) in ((3072, 1024), (1024, 1024), (5248, 1024), (1024, 2624))]
+
+
+def _spin():
+    """Queues a few milliseconds of GPU spinning, so that the host enqueues the timed calls while the
+    GPU is busy and they then run back to back (small GEMMs would otherwise wait on the host)."""
+    import torch
+    torch.cuda._sleep(20_000_000)
+
+
+def _time(fn, iters=20):
+    """Device time per call of fn (us), over back-to-back calls bracketed by events."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _spin()
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters * 1e3                # us per call
+
+
+def c2(lib):
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(0)
+    ws = torch.empty(64 << 20, dtype=torch.float32, device="cuda")   # split-K partials (256 MiB)
+    print("| M | N | K | dtype | torch.mm us | TFLOP/s | engine us | TFLOP/s | engine plan | planner us | max rel err vs torch.mm |")
+    print("|---:|---:|---:|---|---:|---:|---:|---:|---|---:|---:|")
+    for (M, N, K) in C2_SHAPES:
+        fl = 2.0 * M * N * K
+        A32 = torch.randn(M, K, generator=g).cuda()
+        W32 = (torch.randn(N, K, generator=g) * 0.02).cuda()
+        for dt in (torch.bfloat16, torch.float32):
+            A, W = A32.to(dt), W32.to(dt)
+            Wt = W.t()
+            ref = torch.empty(M, N, dtype=dt, device="cuda")
+            t_mm = _time(lambda: torch.mm(A, Wt, out=ref))
+            C = torch.empty(M, N, dtype=dt, device="cuda")
+            plans = [(-1, 1)]
+            if dt == torch.bfloat16:
+                plans += [(c, 1) for c in range(8)]
+                if M <= 4096:
+                    plans += [(c, ks) for ks in (2, 4, 8) if K % (64 * ks) == 0 for c in range(8)]
+            best, t_plan = None, None
+            for cfg, ks in plans:
+                le.gemm_config(lib, cfg)
+                le.gemm_ksplit(lib, ks if ks > 1 else 0, ws if ks > 1 else None)
+                le.gemm(lib, A, W, C)                      # warm-up
+                _spin()
+                t = le.gemm(lib, A, W, C, iters=20) / 20 * 1e3  # back-to-back launches, device events
+                err = ((C.float() - ref.float()).abs().max() / ref.float().abs().max()).item()
+                if cfg == -1:
+                    t_plan = t
+                if best is None or t < best[0]:
+                    best = (t, cfg, ks, err)
+            le.gemm_config(lib, -1)
+            le.gemm_ksplit(lib, 0, None)
+            t, cfg, ks, err = best
+            plan = "planner" if cfg == -1 else "cfg %d%s" % (cfg, ", split-K %d" % ks if ks > 1 else "")
+            print("| %d | %d | %d | %s | %.1f | %.0f | %.1f | %.0f | %s | %.1f | %.1e |"
+                  % (M, N, K, "bf16" if dt == torch.bfloat16 else "fp32", t_mm, fl / t_mm / 1e6, t, fl / t / 1e6, plan,
+                     t_plan, err), flush=True)
 
 
 def main():
@@ -20,9 +95,13 @@ def main():
     ap.add_argument("--K", type=int, default=4096)
     ap.add_argument("--cfg", type=int, default=0)
     ap.add_argument("--iters", type=int, default=4)
+    ap.add_argument("--c2", action="store_true", help="time the microbenchmark shapes against torch.mm")
     a = ap.parse_args()
     lib = le.load_library()
     import torch
+    if a.c2:
+        c2(lib)
+        return
     g = torch.Generator(device="cpu").manual_seed(0)
     A = torch.randn(a.M, a.K, generator=g).to(torch.bfloat16).cuda()
     W = (torch.randn(a.N, a.K, generator=g) * 0.02).to(torch.bfloat16).cuda()
