@@ -825,19 +825,21 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       float* tsin = tcos + BM * 32;
       if (rope) {
         // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
-        // four 16-byte pieces per thread at a time (the positions were loaded before the K loop)
+        // NB 16-byte pieces of each per thread at a time: all of them (one round trip) up to 192
+        // rows, else four (the positions were loaded before the K loop)
+        constexpr int NB = NT <= 6 ? NT : 4;
 #pragma unroll
-        for (int k0 = 0; k0 < NT; k0 += 4) {
-          float4 tc[4], ts[4];
+        for (int k0 = 0; k0 < NT; k0 += NB) {
+          float4 tc[NB], ts[NB];
 #pragma unroll
-          for (int k = 0; k < 4; k++) {
+          for (int k = 0; k < NB; k++) {
             if (k0 + k >= NT) break;
             const int q = (tid + 256 * (k0 + k)) & 7;
             tc[k] = *reinterpret_cast<const float4*>(a.rope_cos + pp[k0 + k] * 32 + 4 * q);
             ts[k] = *reinterpret_cast<const float4*>(a.rope_sin + pp[k0 + k] * 32 + 4 * q);
           }
 #pragma unroll
-          for (int k = 0; k < 4; k++) {
+          for (int k = 0; k < NB; k++) {
             if (k0 + k >= NT) break;
             const int it = tid + 256 * (k0 + k), r = it >> 3, q = it & 7;
             *reinterpret_cast<float4*>(tcos + r * 32 + 4 * q) = tc[k];
