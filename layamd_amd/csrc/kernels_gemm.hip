@@ -411,12 +411,13 @@ __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32
 // over three sub-steps leaves the last part too little time to land before the wait.  Every stage
 // but the last issues the same DMA instructions (past the last stage they read nothing), so the
 // wait is a constant vmcnt(0).  K is a multiple of 64 (every stage is whole).
-template <bool SWAP, int FM, int FN, int PA, int PB, class ST>
+template <bool SWAP, int NX, int FM, int FN, int PA, int PB, class ST>
 __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST& T1, const XlDma64<PA, PB>& d, int arow,
                                             int brow, int hi, int sw) {
   constexpr int NMM = FM * FN, E = FM + FN, EW = PB + FM + FN, EA = PA + FM + FN;
   Frags<FM, FN> F0, F1;
-  LAYA_WAIT_VMCNT(PA);                     // stage 0 (the A part of stage 1 may still be in flight)
+  // stage 0; the A part of stage 1 and NX later fills the caller issued may still be in flight
+  LAYA_WAIT_VMCNT(PA + NX);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -567,10 +568,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   static_assert(!RING || BM * BN <= 128 * 128, "the ring loop is for two workgroups per CU");
   constexpr int SA = BMQ * 8, SW = BN * 8;               // buffer sizes in 16-byte chunks
   struct Stage64 { u32x4_t a[SA]; u32x4_t b[SW]; };
-  __shared__ u32x4_t L[RING ? 3 * SA + 2 * SW : 2 * (SA + SW)];
+  constexpr int NST = RING ? 3 * SA + 2 * SW : 2 * (SA + SW);
+  // QKV projection (two K buffers): the RoPE tables of the tile's rows ([BM][32] floats of cos,
+  // then of sin) get LDS of their own where it fits, and are fetched during the K loop
+  constexpr bool PRE = EPI == EPI_QKV && !RING && (NST + BM * 16) * 16 < 160 * 1024;
+  __shared__ u32x4_t L[NST + (PRE ? BM * 16 : 0)];
   constexpr int BMP = (BM + 63) / 64 * 64;
   constexpr int SB = (BMP + BN) * 16;                    // staging bytes per wave
-  static_assert(4 * SB + (EPI == EPI_QKV ? 2 * BM * 32 * 4 : 0) <= (int)sizeof(L), "epilogue LDS");
+  static_assert(4 * SB + (EPI == EPI_QKV && !PRE ? 2 * BM * 32 * 4 : 0) <= NST * 16, "epilogue LDS");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -594,12 +599,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // first so that they are the oldest loads (the K loop's counted waits then never wait on them)
   // and the epilogue can issue its table loads at once
   constexpr int NT = BM * 8 / 256;
+  constexpr int NTX = PRE ? 2 * NT : 0;                  // RoPE table fills issued after stage 1's A part
+  // Loaded without a branch, through a buffer resource that has no records when the tile needs no
+  // tables (the loads then read 0 and touch no memory): loads in a conditional block make the
+  // compiler wait for them where the block ends, before the K stages are even requested.
   int pp[EPI == EPI_QKV ? NT : 1];
   if constexpr (EPI == EPI_QKV) {
-    if (swap && a.rope_cos != nullptr) {
+    const bool need = swap && a.rope_cos != nullptr;
+    const __amdgpu_buffer_rsrc_t rpos =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(a.pos), (short)0, need ? a.M * 4 : 0, 0x00020000);
 #pragma unroll
-      for (int k = 0; k < NT; k++) pp[k] = a.pos[min(m0 + ((tid + 256 * k) >> 3), a.M - 1)];
-    }
+    for (int k = 0; k < NT; k++)
+      pp[k] = __builtin_amdgcn_raw_buffer_load_b32(rpos, min(m0 + ((tid + 256 * k) >> 3), a.M - 1) * 4, 0, 0);
   }
 
   XlDma64<PA, PB> dm;
@@ -629,6 +640,32 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     for (int o = 0; o < PB; o++) dm.op_b(o, lds_addr(T0.b), 0);
 #pragma unroll
     for (int o = 0; o < PA; o++) dm.op_a(o, lds_addr(T1.a), 1);
+    if constexpr (PRE) {
+      // RoPE table rows: piece k of this thread is row r = (tid + 256 k) / 8, 16-byte chunk tid % 8,
+      // so one DMA instruction of wave w fills rows 32 k + 8 w .. + 7, i.e. LDS bytes
+      // (4 k + w) * 1024 on; the K loop's first wait leaves these in flight, its second covers them
+      // Issued by every tile, without a branch (a tile that needs no tables reads through
+      // resources without records: nothing is read, and the K loop's first wait count holds).
+      const bool need = swap && a.rope_cos != nullptr;
+      const u32x4_t rc = need ? make_rsrc(a.rope_cos, 0xFFFFFFF0u) : dm.rNone;
+      const u32x4_t rs = need ? make_rsrc(a.rope_sin, 0xFFFFFFF0u) : dm.rNone;
+      const uint32_t tc = lds_addr(L + NST), ts = tc + BM * 128;
+      const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+      // All offsets first, each pinned by an empty statement that uses it: the compiler's waits for
+      // the position loads (which in hardware also wait for every fill issued after them) then
+      // come together here, not between table fills, where each would wait for the fills before it.
+      uint32_t voff[NT];
+#pragma unroll
+      for (int k = 0; k < NT; k++) {
+        voff[k] = (uint32_t)pp[k] * 128u + (uint32_t)(lane & 7) * 16u;
+        asm volatile("" ::"v"(voff[k]));
+      }
+#pragma unroll
+      for (int k = 0; k < NT; k++) {
+        dma16(rc, tc + (4u * k + w) * 1024u, voff[k], 0u);
+        dma16(rs, ts + (4u * k + w) * 1024u, voff[k], 0u);
+      }
+    }
   } else {
     const uint32_t l0 = lds_addr(L);
 #pragma unroll
@@ -689,8 +726,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
     else xl_k_loop64r<false, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
   } else {
-    if (swap) xl_k_loop64<true>(acc, T0, T1, dm, arow, brow, hi, sw);
-    else xl_k_loop64<false>(acc, T0, T1, dm, arow, brow, hi, sw);
+    if (swap) xl_k_loop64<true, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
+    else xl_k_loop64<false, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
   }
 
   // ---------------- epilogue ----------------
@@ -821,9 +858,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       constexpr int CW = fitw(WTN, SB / 64), CPR = CW / 8;
       static_assert(CW % 64 == 0, "whole heads per staged block");
       const bool rope = a.rope_cos != nullptr;
-      float* tcos = reinterpret_cast<float*>(reinterpret_cast<char*>(L) + 4 * SB);
+      float* tcos = PRE ? reinterpret_cast<float*>(L + NST) : reinterpret_cast<float*>(reinterpret_cast<char*>(L) + 4 * SB);
       float* tsin = tcos + BM * 32;
-      if (rope) {
+      if (rope && !PRE) {
         // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
         // NB 16-byte pieces of each per thread at a time: all of them (one round trip) up to 192
         // rows, else four (the positions were loaded before the K loop)
@@ -852,7 +889,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       for (int j = 0; j < FN; j++)
 #pragma unroll
         for (int g = 0; g < 4; g++) if constexpr (HB) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
-      if (rope) __syncthreads();                          // tables complete
+      if (rope && !PRE) __syncthreads();                  // tables complete
       T* dst = reinterpret_cast<T*>(cbase < D ? a.Q : a.Kt) + (cbase % D);
 #pragma unroll
       for (int i = 0; i < FM; i++) {
