@@ -96,6 +96,8 @@ def main():
     ap.add_argument("--cfg", type=int, default=0)
     ap.add_argument("--iters", type=int, default=4)
     ap.add_argument("--c2", action="store_true", help="time the microbenchmark shapes against torch.mm")
+    ap.add_argument("--torch", action="store_true",
+                    help="after the engine launches, run torch.mm on the same operands as many times")
     a = ap.parse_args()
     lib = le.load_library()
     import torch
@@ -116,6 +118,11 @@ def main():
     per = ms / a.iters
     print("gemm %dx%dx%d cfg %d: %.1f us per launch (%.1f ms wall for %d), %.0f TFLOP/s"
           % (a.M, a.N, a.K, a.cfg, per * 1e3, wall, a.iters, 2.0 * a.M * a.N * a.K / (per * 1e-3) / 1e12))
+    if a.torch:
+        Wt = W.t()
+        torch.mm(A, Wt, out=C)                             # warm-up
+        t = _time(lambda: torch.mm(A, Wt, out=C), a.iters)
+        print("torch.mm %dx%dx%d: %.1f us per call, %.0f TFLOP/s" % (a.M, a.N, a.K, t, 2.0 * a.M * a.N * a.K / t / 1e6))
 
 
 if __name__ == "__main__":
