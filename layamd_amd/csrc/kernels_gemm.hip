@@ -1308,7 +1308,22 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
       if (cfg >= 0) { launch_xl_cfg(epi, a, cfg, st); return; }
     }
   }
-  launch_cfg<T, 128, 128, 2, 2>(epi, a, st);
+  // fp32 (and bf16 shapes the MFMA path above cannot take): 128x128 tiles when they fill the chip,
+  // else 64x64 tiles (waves 4x1, so each wave still holds whole 64-column groups for the GeGLU and
+  // RoPE pairings) for four times the workgroups.  Every output's K order is the same in all of
+  // them, so the choice changes no bits and a row's result does not depend on the batch.
+  // Stores and residual updates whose 64x64 tiles still leave CUs idle take 32x64 tiles.
+  const int tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  const int tiles64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+  if (tiles128 >= num_cus()) {
+    launch_cfg<T, 128, 128, 2, 2>(epi, a, st);
+  } else if (tiles64 < num_cus() && (epi == EPI_STORE || epi == EPI_RESID)) {
+    const int tiles = ((a.M + 31) / 32) * ((a.N + 63) / 64);
+    if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm<T, 32, 64, 2, 2, EPI_STORE>), dim3(tiles), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_gemm<T, 32, 64, 2, 2, EPI_RESID>), dim3(tiles), dim3(256), 0, st, a);
+  } else {
+    launch_cfg<T, 64, 64, 4, 1>(epi, a, st);
+  }
 }
 
 template void launch_gemm<float>(int, const GemmArgs&, hipStream_t);

@@ -140,6 +140,34 @@ def test_gemm_ring_bit_identical_to_two_buffer_loop():
     assert torch.equal(X1[:part].cpu(), X2.cpu())
 
 
+@pytest.mark.parametrize("part", [64, 1024])
+def test_fp32_gemm_rows_independent_of_tiling(part):
+    """fp32 GEMM: the first rows give the same bits in a grid of 128x128 tiles that fills the chip
+    and alone, in a grid of smaller tiles (64 rows: 32x64 tiles; 1024 rows: 64x64), for a GELU
+    store and a residual update: a row's result does not depend on the batch around it."""
+    import torch
+    lib = le.load_library()
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    N, K = 1024, 2624
+    M = 128 * (ncu // (N // 128) + 1)
+    g = torch.Generator(device="cpu").manual_seed(6)
+    A = torch.randn(M, K, generator=g).cuda()
+    W = (torch.randn(N, K, generator=g) * 0.02).cuda()
+    b = (torch.randn(N, generator=g) * 0.1).cuda()
+    X0 = torch.randn(M, N, generator=g).cuda()
+    C1 = torch.zeros(M, N, device="cuda")
+    le.gemm(lib, A, W, C1, bias=b, act=2)
+    C2 = torch.zeros(part, N, device="cuda")
+    le.gemm(lib, A[:part].contiguous(), W, C2, bias=b, act=2)
+    X1 = X0.clone()
+    le.gemm(lib, A, W, X1, bias=b, residual=True)
+    X2 = X0[:part].clone()
+    le.gemm(lib, A[:part].contiguous(), W, X2, bias=b, residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(C1[:part].cpu(), C2.cpu())
+    assert torch.equal(X1[:part].cpu(), X2.cpu())
+
+
 def test_mfma_loop_probe():
     """The achievable-peak probe runs and reports a rate between a tenth of the published bf16
     peak and the peak itself (the chip cannot beat 2.5166 PF; a broken probe reads far lower)."""
