@@ -551,8 +551,72 @@ __device__ __forceinline__ void xl_k_loop64r(f32x16_t (&acc)[FM][FN], const u32x
   LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
 }
 
-// RING: the three-A-buffer K loop, for 128x128 tiles when the grid puts two workgroups on a CU
-template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, bool RING>
+// The K loop for grids of 128x128 tiles that leave CUs without a second workgroup (a few hundred
+// rows): NB whole stage buffers, NB - 1 stages issued ahead, so a fill has NB - 2 stages of
+// multiplication to land in, not one.  With so few tiles a stage's MFMAs (a quarter of a
+// microsecond) are far shorter than a fill's trip to L2 or HBM, and the two-buffer loop waited
+// that trip out at every stage.  Stage g lives in buffer g % NB.  Each iteration waits until stage g
+// has landed (the NB - 2 later stages may still be in flight: every stage issues the same PA + PB
+// DMA instructions, past the last one from a resource without records), passes one barrier (after
+// which no wave still reads stage g - 1's buffer) and refills that buffer with stage g + NB - 1:
+// the A part between the first sub-step's MFMAs, the W part between the second's.  The K order of
+// every accumulator is the one of the other loops, so the bits are too.
+template <bool SWAP, int FM, int FN, int PA, int PB, int SA, int SW, int NB>
+__device__ __forceinline__ void xl_k_loop64d(f32x16_t (&acc)[FM][FN], const u32x4_t* L, const XlDma64<PA, PB>& d,
+                                             int arow, int brow, int hi, int sw) {
+  constexpr int PS = PA + PB, NMM = FM * FN, E = FM + FN, EA = PA + FM + FN, EW = PB + FM + FN, SS = SA + SW;
+  const uint32_t l0 = lds_addr(L);
+  Frags<FM, FN> F0, F1;
+  const int nst = d.ns / 2;
+  int b = 0;                               // buffer of stage g
+  for (int g = 0; g < nst; g++) {
+    LAYA_WAIT_VMCNT((NB - 2) * PS);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int bp = b == 0 ? NB - 1 : b - 1;
+    const uint32_t la = l0 + (uint32_t)(bp * SS * 16), lb = la + (uint32_t)(SA * 16);
+    const u32x4_t* CA = L + b * SS;
+    const u32x4_t* CB = CA + SA;
+#pragma unroll
+    for (int o = 0; o < E; o++) load_frag64(F0, o, CA, CB, arow, brow, 0, hi, sw);
+#pragma unroll
+    for (int t = 0; t < NMM; t++) {
+      mma_one_x<SWAP>(acc, F0, t);
+#pragma unroll
+      for (int o = t * EA / NMM; o < (t + 1) * EA / NMM; o++) {
+        if (o < PA) d.op_a(o, la, g + NB - 1);
+        else load_frag64(F1, o - PA, CA, CB, arow, brow, 1, hi, sw);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < NMM; t++) {
+      mma_one_x<SWAP>(acc, F1, t);
+#pragma unroll
+      for (int o = t * EW / NMM; o < (t + 1) * EW / NMM; o++) {
+        if (o < PB) d.op_b(o, lb, g + NB - 1);
+        else load_frag64(F0, o - PB, CA, CB, arow, brow, 2, hi, sw);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < NMM; t++) {
+      mma_one_x<SWAP>(acc, F0, t);
+#pragma unroll
+      for (int o = t * E / NMM; o < (t + 1) * E / NMM; o++) load_frag64(F1, o, CA, CB, arow, brow, 3, hi, sw);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);
+    b = b + 1 == NB ? 0 : b + 1;
+  }
+  LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
+}
+
+// LOOP: the K loop.  0: two stage buffers (one workgroup per CU); 1 (128x128 tiles when the grid
+// puts two workgroups on a CU): three A buffers and two W buffers; 2 (128x128 tiles, grid of at most
+// one workgroup per CU): four stage buffers, two stages of lead.
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -565,13 +629,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // K stages: two whole stages (A then W part), or (RING) three A buffers and two W buffers (BMQ and
   // BN rows of 128 bytes); after the K loop the same memory holds the epilogue's staging area (SB
   // bytes per wave) and, for the QKV projection, the RoPE tables of the tile's rows
-  static_assert(!RING || BM * BN <= 128 * 128, "the ring loop is for two workgroups per CU");
+  static_assert(LOOP == 0 || BM * BN <= 128 * 128, "the ring and deep loops are for 128x128 tiles");
+  constexpr bool RING = LOOP == 1;
+  constexpr int NBD = 4;                                 // stage buffers of the deep loop
   constexpr int SA = BMQ * 8, SW = BN * 8;               // buffer sizes in 16-byte chunks
   struct Stage64 { u32x4_t a[SA]; u32x4_t b[SW]; };
-  constexpr int NST = RING ? 3 * SA + 2 * SW : 2 * (SA + SW);
+  constexpr int NST = RING ? 3 * SA + 2 * SW : LOOP == 2 ? NBD * (SA + SW) : 2 * (SA + SW);
   // QKV projection (two K buffers): the RoPE tables of the tile's rows ([BM][32] floats of cos,
   // then of sin) get LDS of their own where it fits, and are fetched during the K loop
-  constexpr bool PRE = EPI == EPI_QKV && !RING && (NST + BM * 16) * 16 < 160 * 1024;
+  constexpr bool PRE = EPI == EPI_QKV && LOOP == 0 && (NST + BM * 16) * 16 < 160 * 1024;
   __shared__ u32x4_t L[NST + (PRE ? BM * 16 : 0)];
   constexpr int BMP = (BM + 63) / 64 * 64;
   constexpr int SB = (BMP + BN) * 16;                    // staging bytes per wave
@@ -632,7 +698,17 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   dm.ns = a.K / 32;
   Stage64& T0 = *reinterpret_cast<Stage64*>(L);
   Stage64& T1 = *reinterpret_cast<Stage64*>(L + SA + SW);
-  if constexpr (!RING) {
+  if constexpr (LOOP == 2) {
+    // stages 0 .. NBD - 2 into buffers 0 .. NBD - 2
+#pragma unroll
+    for (int g = 0; g < NBD - 1; g++) {
+      const uint32_t lg = lds_addr(L) + (uint32_t)(g * (SA + SW) * 16);
+#pragma unroll
+      for (int o = 0; o < PA; o++) dm.op_a(o, lg, g);
+#pragma unroll
+      for (int o = 0; o < PB; o++) dm.op_b(o, lg + SA * 16, g);
+    }
+  } else if constexpr (!RING) {
     // stage 0, then the A part of stage 1 (the K loop's first sub-step issues its W part)
 #pragma unroll
     for (int o = 0; o < PA; o++) dm.op_a(o, lds_addr(T0.a), 0);
@@ -725,6 +801,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   if constexpr (RING) {
     if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
     else xl_k_loop64r<false, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
+  } else if constexpr (LOOP == 2) {
+    if (swap) xl_k_loop64d<true, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
+    else xl_k_loop64d<false, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
   } else {
     if (swap) xl_k_loop64<true, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
     else xl_k_loop64<false, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
@@ -1014,22 +1093,25 @@ static int num_cus() {
   return n;
 }
 
-template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool RING>
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, int LOOP>
 static void launch_xl_ring(const GemmArgs& a, int tiles, hipStream_t st) {
-  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, RING>), dim3(tiles), dim3(256), 0, st, a);
-  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, RING>), dim3(tiles), dim3(256), 0, st, a);
+  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP>), dim3(tiles), dim3(256), 0, st, a);
+  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP>), dim3(tiles), dim3(256), 0, st, a);
 }
 
 // 128x128 tiles take the three-A-buffer loop when the grid has more tiles than the chip has CUs,
-// i.e. when CUs run two workgroups whose stages interleave; with one workgroup per CU the
-// two-buffer loop is faster.  Both give the same bits.
+// i.e. when CUs run two workgroups whose stages interleave, and the four-buffer loop otherwise
+// (one workgroup per CU, few tiles: the fill latency is what a stage waits for).  Other tiles take
+// the two-buffer loop.  All give the same bits.
 template <int BM, int BN, int WM, int WN, int EPI, int ACT>
 static void launch_xl_hb(const GemmArgs& a, hipStream_t st) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (EPI == EPI_PARTIAL ? a.ksplit : 1);
   if constexpr (BM * BN <= 128 * 128) {
-    if (tiles > num_cus()) { launch_xl_ring<BM, BN, WM, WN, EPI, ACT, true>(a, tiles, st); return; }
+    if (tiles > num_cus()) launch_xl_ring<BM, BN, WM, WN, EPI, ACT, 1>(a, tiles, st);
+    else launch_xl_ring<BM, BN, WM, WN, EPI, ACT, 2>(a, tiles, st);
+    return;
   }
-  launch_xl_ring<BM, BN, WM, WN, EPI, ACT, false>(a, tiles, st);
+  launch_xl_ring<BM, BN, WM, WN, EPI, ACT, 0>(a, tiles, st);
 }
 
 template <int BM, int BN, int WM, int WN>

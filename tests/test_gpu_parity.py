@@ -93,7 +93,7 @@ def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
 
 
 # 128x128 tiles run the three-A-buffer K loop when the grid has more tiles than the chip has CUs
-# (two workgroups per CU), the two-buffer loop otherwise
+# (two workgroups per CU), the four-buffer loop otherwise
 def _ring_rows(n_tiles_per_row):
     import torch
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
@@ -111,9 +111,9 @@ def test_gemm_ring_vs_torch(N, K):
         le.gemm_config(lib, prev)
 
 
-def test_gemm_ring_bit_identical_to_two_buffer_loop():
+def test_gemm_ring_bit_identical_to_four_buffer_loop():
     """The first rows of a GEMM give the same bits through the ring loop (a grid of more 128x128
-    tiles than CUs) and through the two-buffer loop (the same rows alone, a grid of fewer), for a
+    tiles than CUs) and through the four-buffer loop (the same rows alone, a grid of fewer), for a
     GELU store and a residual update."""
     import torch
     lib = le.load_library()
