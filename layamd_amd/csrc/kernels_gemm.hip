@@ -7,14 +7,16 @@
 //
 //   k_gemm_xl  bf16, the engine's path.  256-thread workgroups, tiles from 128x128 to 256x256 on
 //              v_mfma_f32_32x32x16_bf16; K advances in 64-deep stages (whole 128-byte lines of
-//              every tile row), two in LDS, filled one ahead by LDS DMA (buffer_load ... lds);
-//              the product is computed
+//              every tile row), filled ahead by LDS DMA (buffer_load ... lds): two stage buffers,
+//              or for 128x128 tiles three A buffers (two workgroups per CU) or four stage buffers
+//              (grids of at most one tile per CU).  The product is computed
 //              transposed so each lane holds four consecutive output columns; the epilogue is
 //              staged through LDS and leaves as full-line 16-byte stores.  The engine picks the
 //              tile shape (and an optional row split over two launches) per GEMM by timing.
 //   k_gemm     fp32 operands, and bf16 shapes the tiled kernel cannot take (unaligned N or
-//              strides).  128x128 tiles, K in 128-byte slices through double-buffered LDS with
-//              register prefetch, v_mfma_f32_16x16x4_f32 / v_mfma_f32_16x16x32_bf16.
+//              strides).  128x128, 64x64 or 32x64 tiles by how many fill the chip, K in 128-byte
+//              slices through double-buffered LDS with register prefetch,
+//              v_mfma_f32_16x16x4_f32 / v_mfma_f32_16x16x32_bf16.
 //
 // Both remap workgroup ids so each of the 8 XCDs (own L2) walks a contiguous run of tiles.
 //
