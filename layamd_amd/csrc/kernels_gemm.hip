@@ -724,6 +724,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       // (4 k + w) * 1024 on; the K loop's first wait leaves these in flight, its second covers them
       // Issued by every tile, without a branch (a tile that needs no tables reads through
       // resources without records: nothing is read, and the K loop's first wait count holds).
+      // The table resources do not bound the rows: positions come from the host's packing, which
+      // keeps them below the tables' row count (the length limit plus the padding rows).
       const bool need = swap && a.rope_cos != nullptr;
       const u32x4_t rc = need ? make_rsrc(a.rope_cos, 0xFFFFFFF0u) : dm.rNone;
       const u32x4_t rs = need ? make_rsrc(a.rope_sin, 0xFFFFFFF0u) : dm.rNone;
