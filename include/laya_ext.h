@@ -44,14 +44,14 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
 int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* flops);
 
 /* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 lets the planner
- * choose per GEMM (the default, or LAYA_GEMM_CFG); 0..7 select 256x256, 256x128, 128x256, 128x128,
- * 192x256, 160x256, 128x192 or 192x128 tiles (the QKV projection falls back to a shape that keeps its tiles inside one of
+ * choose per GEMM (the default, or LAYA_GEMM_CFG); 0..8 select 256x256, 256x128, 128x256, 128x128,
+ * 192x256, 160x256, 128x192, 192x128 or 128x64 tiles (the QKV projection falls back to a shape that keeps its tiles inside one of
  * the q/k/v sections).  Passes already captured in HIP graphs keep their kernels.  Returns the
  * previous setting, or -2 for an invalid value. */
 int laya_ext_gemm_config(int cfg);
 
 /* Row split used with the pinned configuration: rows [split_rows, M) of every later pinned launch
- * run as a second launch with tile configuration cfg_tail (0..7); split_rows 0 removes the split.
+ * run as a second launch with tile configuration cfg_tail (0..8); split_rows 0 removes the split.
  * A split the shape cannot take (split_rows >= M, not a multiple of 8, a tail configuration the
  * shape cannot use) runs as one launch.  Returns 0, or -2 for an invalid value. */
 int laya_ext_gemm_split(int split_rows, int cfg_tail);

@@ -57,8 +57,8 @@ struct GemmArgs {
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
-// pins the bf16 tile configuration for later launches (-1: the planner; 0..7: 256x256, 256x128,
-// 128x256, 128x128, 192x256, 160x256, 128x192, 192x128); returns the previous setting
+// pins the bf16 tile configuration for later launches (-1: the planner; 0..8: 256x256, 256x128,
+// 128x256, 128x128, 192x256, 160x256, 128x192, 192x128, 128x64); returns the previous setting
 int gemm_config(int cfg);
 int gemm_pinned();                               // the pinned configuration, or -1
 // row split used together with the pinned configuration: rows [split_rows, M) run as a second
@@ -67,7 +67,7 @@ void gemm_pin_split(int split_rows, int cfg_tail);
 // split-K factor applied to later bf16 EPI_STORE / EPI_RESID launches that name none (<= 1: none);
 // returns the previous one
 int gemm_pin_ksplit(int ks);
-constexpr int kGemmConfigs = 8;
+constexpr int kGemmConfigs = 9;
 // the achievable-MFMA probe: blocks x 4 waves, each iters x 8 MFMAs of 32x32x16 bf16 (32768 flop);
 // out holds blocks x 256 floats
 void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st);

@@ -642,7 +642,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   constexpr bool PRE = EPI == EPI_QKV && LOOP == 0 && (NST + BM * 16) * 16 < 160 * 1024;
   __shared__ u32x4_t L[NST + (PRE ? BM * 16 : 0)];
   constexpr int BMP = (BM + 63) / 64 * 64;
-  constexpr int SB = (BMP + BN) * 16;                    // staging bytes per wave
+  // staging bytes per wave: at least a block of 32 rows x 32 fp32 columns, so every epilogue
+  // stages whole 32-column accumulator blocks
+  constexpr int SB = (BMP + BN) * 16 > 32 * 32 * 4 ? (BMP + BN) * 16 : 32 * 32 * 4;
   static_assert(4 * SB + (EPI == EPI_QKV && !PRE ? 2 * BM * 32 * 4 : 0) <= NST * 16, "epilogue LDS");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
@@ -863,6 +865,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     // fp32: blocks of 32 rows x CW columns (split-K partials go to their chunk's slice of X)
     float* const xo = EPI == EPI_PARTIAL ? a.X + (size_t)split * a.M * a.ldx : a.X;
     constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
+    static_assert(CW % 32 == 0, "whole accumulator blocks per staged block");
     float4 bb[FN][4] = {};
 #pragma unroll
     for (int j = 0; j < FN; j++)
@@ -893,6 +896,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     // bf16 rows of OW output columns, blocks of 32 rows x CW columns
     constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;
     constexpr int CW = fitw(OW, SB / 64), CPR = CW / 8;
+    static_assert(CW % 32 == 0, "whole accumulator blocks per staged block");
     const int ocol = EPI == EPI_GEGLU ? cbase / 2 : cbase, ncol = EPI == EPI_GEGLU ? a.N / 2 : a.N;
     // bias per (column block, e / 4): input and gate parts for GeGLU
     float4 bx[FN][4] = {};
@@ -1149,7 +1153,7 @@ static void launch_xl(int epi, const GemmArgs& a, hipStream_t st) {
 struct XlCfg { int bm, bn, per_cu; float rel; };
 static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80f}, {128, 256, 1, 0.83f},
                                         {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}, {160, 256, 1, 0.93f},
-                                        {128, 192, 2, 0.80f}, {192, 128, 2, 0.80f}};
+                                        {128, 192, 2, 0.80f}, {192, 128, 2, 0.80f}, {128, 64, 2, 0.50f}};
 
 // tile configuration pinned for every bf16 launch (-1: none); LAYA_GEMM_CFG sets it at the first
 // launch, gemm_config() at run time
@@ -1281,6 +1285,7 @@ static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
     case 5: launch_xl<160, 256, 1, 4>(epi, a, st); return;
     case 6: launch_xl<128, 192, 4, 1>(epi, a, st); return;
     case 7: launch_xl<192, 128, 2, 2>(epi, a, st); return;
+    case 8: launch_xl<128, 64, 4, 1>(epi, a, st); return;
     default: fprintf(stderr, "[laya] gemm: bad tile configuration %d\n", cfg); exit(1);
   }
 }

@@ -107,7 +107,7 @@ def gemm(lib, A, W, C, bias=None, act=0, residual=False, stream=None, iters=1):
 
 
 def gemm_config(lib, cfg: int) -> int:
-    """Pins the bf16 GEMM tile configuration (-1: planner, 0..7: see laya_ext.h); returns the previous."""
+    """Pins the bf16 GEMM tile configuration (-1: planner, 0..8: see laya_ext.h); returns the previous."""
     prev = lib.laya_ext_gemm_config(cfg)
     if prev == -2:
         raise ValueError("invalid GEMM configuration %d" % cfg)

@@ -4,7 +4,7 @@ runs (rocprofv3 --pmc) of a single kernel:
     python -m layamd_amd.gemm_probe --M 16384 --N 4096 --K 4096 --cfg 0 --iters 4
 
 A = N(0,1) and W = N(0,0.02) in bf16, C = A W^T stored in bf16 (plain epilogue, no bias).  --cfg
-pins the tile configuration (0..7, see include/laya_ext.h; -1: the planner).  Prints the time per
+pins the tile configuration (0..8, see include/laya_ext.h; -1: the planner).  Prints the time per
 launch and the TFLOP/s on 2 M N K flop.
 
     python -m layamd_amd.gemm_probe --c2
@@ -64,9 +64,9 @@ def c2(lib):
             C = torch.empty(M, N, dtype=dt, device="cuda")
             plans = [(-1, 1)]
             if dt == torch.bfloat16:
-                plans += [(c, 1) for c in range(8)]
+                plans += [(c, 1) for c in range(9)]
                 if M <= 4096:
-                    plans += [(c, ks) for ks in (2, 4, 8) if K % (64 * ks) == 0 for c in range(8)]
+                    plans += [(c, ks) for ks in (2, 4, 8) if K % (64 * ks) == 0 for c in range(9)]
             best, t_plan = None, None
             for cfg, ks in plans:
                 le.gemm_config(lib, cfg)

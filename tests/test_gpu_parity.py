@@ -65,7 +65,7 @@ def golden_flat_logits(c):
 
 # ---------------------------------------------------------------- GEMM kernel vs torch fp32
 # bf16 runs every tile configuration of the MFMA GEMM (-1: the planner's choice)
-@pytest.mark.parametrize("dtype,cfg", [("fp32", -1)] + [("bf16", c) for c in (-1, 0, 1, 2, 3, 4, 5, 6, 7)])
+@pytest.mark.parametrize("dtype,cfg", [("fp32", -1)] + [("bf16", c) for c in (-1, 0, 1, 2, 3, 4, 5, 6, 7, 8)])
 @pytest.mark.parametrize("M,N,K", [(1, 128, 64), (17, 256, 128), (128, 128, 1024), (300, 384, 192), (200, 256, 320),
                                    (513, 1024, 2624)])
 def test_gemm_vs_torch(dtype, cfg, M, N, K):
@@ -443,7 +443,7 @@ def test_tile_configs_bit_identical():
     prev = le.gemm_config(e.lib, -1)
     try:
         ref_lo, ref_ac = e.forward_flat(*b.flat())
-        for cfg in (0, 1, 2, 3, 4, 5, 6, 7):
+        for cfg in (0, 1, 2, 3, 4, 5, 6, 7, 8):
             le.gemm_config(e.lib, cfg)
             lo, ac = e.forward_flat(*b.flat())
             assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
