@@ -307,6 +307,9 @@ struct Engine : EngineIface {
     lim.pass_tokens = std::min(std::max(env_int("LAYA_PASS_TOKENS", lim.pass_tokens), cfg.max_len), lim.pass_tokens);
     lim.max_seqs = std::max(1, env_int("LAYA_MAX_SEQS", 512));
     lim.max_grows = std::max(env_int("LAYA_MAX_GATHERED", 32768), kMaxMarkers + 1);
+    // attention query tiles: 64 queries (two waves in bf16); LAYA_ATTN_QTILE=128 gives bf16 128-query
+    // tiles of four waves, same bits, measured slower on sliding-window layers
+    lim.q_tile = sizeof(T) == 2 && env_int("LAYA_ATTN_QTILE", 64) == 128 ? 128 : 64;
     caps = pass_caps(lim);
     MT = caps.rows; RG = caps.grows; VTC = (MT + 64 + 63) / 64 * 64;
     x = dalloc<float>((size_t)MT * D);
@@ -558,8 +561,8 @@ struct Engine : EngineIface {
         GSTAGE("enc:gemm_qkv_rope", gemm(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
-            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen, nullptr,
-                                nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
+            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, lim.q_tile, H, d_soff, d_vlen,
+                                nullptr, nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
         g.X = x; g.ldx = D;
@@ -600,8 +603,8 @@ struct Engine : EngineIface {
         GSTAGE("head:gemm_qkv", gemm(EPI_QKV, g, st));
       }
       if (!last) {
-        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, H, d_soff, d_vlen,
-                                               nullptr, nullptr, 0, scale, st));
+        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, lim.q_tile, H, d_soff,
+                                               d_vlen, nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
         STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
@@ -613,7 +616,7 @@ struct Engine : EngineIface {
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
-        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt, H, d_soff,
+        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt, kQTile, H, d_soff,
                                                         d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
         { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D; splitk(g);

@@ -17,12 +17,14 @@ extern "C" {
 //   rows[3*T] = ids | pos | seq; seqs[5*B+1] = soff(B+1) | vlen | qt | nm | moff
 //   tiles[4*ntiles], gtiles[4*ngtiles], gq[len], grow[R]
 int laya_host_plan(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
-                   int max_len, int pass_tokens, int max_seqs, int max_grows, int vocab, int pad_id, int which, int* dims,
+                   int max_len, int pass_tokens, int max_seqs, int max_grows, int vocab, int pad_id, int q_tile,
+                   int which, int* dims,
                    int* rows, int* seqs, int* tiles, int* gtiles, int* gq, int* grow) {
   PackLimits lim;
   lim.max_len = max_len; lim.pass_tokens = pass_tokens; lim.max_seqs = max_seqs; lim.max_grows = max_grows;
   lim.vocab = vocab;
   lim.pad_id = pad_id;
+  lim.q_tile = q_tile;
   std::vector<PassPlan> ps;
   if (plan_passes(B, lens, ids, nmark, markers, qtypes, lim, &ps) != 0) return -1;
   if (which >= 0 && which < (int)ps.size()) {

@@ -81,15 +81,16 @@ int gemm_config_bn(int cfg);
 int gemm_planned(int epi, const GemmArgs& a);
 
 // ---- attention over packed sequences ----
-// Query tiles from `tiles`; gathered mode when gq != null (queries are gathered rows
+// Query tiles of <= qtile queries from `tiles` (qtile 64, or 128 for bf16 outside gathered mode;
+// anything else aborts); gathered mode when gq != null (queries are gathered rows
 // grow[gq[tile.q0 + r]], outputs go to row gq[...] of O).  window_half = 0: all keys of the
 // sequence; otherwise keys with |i - j| <= window_half.  V^T column = packed row; sequences start
 // on 8-row boundaries and V^T has 64 columns of slack after the last row.  Q and K hold kv_rows
 // rows; V^T has H * 64 rows.
 template <typename T>
 void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt, int ldv, T* O, int ldo,
-                      const AttnTile* tiles, int ntiles, int H, const int* soff, const int* vlen, const int* gq,
-                      const int* grow, int window_half, float scale, hipStream_t st);
+                      const AttnTile* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
+                      const int* gq, const int* grow, int window_half, float scale, hipStream_t st);
 
 // ---- scorer tail and act head ----
 // logits[r] = dot(h[r], w) + b[0]   (fp32 accumulate)

@@ -220,9 +220,15 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 }
 
 // ======================================================================================
-// bf16 attention (v_mfma_f32_32x32x16_bf16).  One 128-thread workgroup owns one query tile (<= 64
-// queries of one sequence) of one head; each of its two waves owns 32 queries, so every K and V^T
-// fragment read from LDS feeds a 32-query MFMA.  Keys advance in blocks of 64, fetched by LDS DMA
+// bf16 attention (v_mfma_f32_32x32x16_bf16).  One workgroup of NW waves owns one query tile (<= 32 NW
+// queries of one sequence) of one head; each wave owns 32 queries, so every K and V^T fragment read
+// from LDS feeds a 32-query MFMA.  NW = 2 (64-query tiles) is the engine's choice.  NW = 4 (128-query
+// tiles, encoder only) walks 256 keys for 128 queries in a sliding-window layer instead of 192 for 64
+// and fetches each key block once per 128 queries in a global one; it measured 3% faster on global
+// layers and 8% slower on sliding ones (a tile's blocks run one after another, and half as many
+// workgroups hide less of each block's fetch latency).  A query's blocks are the same in both
+// tilings but for blocks masked for every query of its wave, which add exact zeros and move no
+// maximum, so both give the same bits.  Keys advance in blocks of 64, fetched by LDS DMA
 // (inline assembly, as in the GEMM): the next block's K while the current block is scored, the next
 // block's V^T (one buffer) after the current PV step, each published by one wait and one barrier.
 //
@@ -258,19 +264,23 @@ __device__ __forceinline__ u32x4_t attn_rsrc(const void* p, uint32_t bytes) {
   return r;
 }
 
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
+template <int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
                                                         int ldqk, int kv_rows, const bf16_t* __restrict__ Vt, int ldv,
                                                         int vt_rows, bf16_t* __restrict__ O, int ldo,
                                                         const AttnTile* __restrict__ tiles, const int* __restrict__ soff,
                                                         const int* __restrict__ vlen, const int* __restrict__ gq,
                                                         const int* __restrict__ grow, int window_half, float scale) {
   constexpr int HD = 64;
+  constexpr int J = 8 / NW;                                // DMA instructions per wave per block
+  static_assert(NW == 2 || NW == 4, "two or four waves");
   // [buffer][row][8 chunks of 16 bytes]: K rows are keys, V^T rows are d; chunk c of row r sits at
   // position c ^ ((r >> 1) & 7), so 16 lanes reading one chunk of 16 consecutive rows hit 16
   // distinct 16-byte bank positions
   // K is double-buffered (the next block's K is fetched while the current one is used); V^T has
   // one buffer, refilled right after the PV step and landing while the next block's scores and
-  // softmax run.  24 KB per workgroup: six workgroups (the VGPR limit) fit a CU.
+  // softmax run.  24 KB per workgroup: the VGPR limit (three waves per SIMD) fits six two-wave or
+  // three four-wave workgroups on a CU.
   __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs[64 * 8];
 
   // heads are the fastest grid dimension, so the (longest-first) tiles start in order
@@ -308,25 +318,25 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 #pragma unroll
   for (int s = 0; s < 4; s++) qf[s] = qrow[2 * s + hi];
 
-  // DMA plan: instruction j (0..3 per wave) fills rows 8 (4 wave + j) .. + 7 of the K block and of
-  // the V^T block; lane -> row + lane / 8, position lane % 8 (global chunk position ^ swizzle)
+  // DMA plan: instruction j (0..J-1 per wave) fills rows 8 (J wave + j) .. + 7 of the K block and
+  // of the V^T block; lane -> row + lane / 8, position lane % 8 (global chunk position ^ swizzle)
   const u32x4_t rK = attn_rsrc(K, (uint32_t)((size_t)kv_rows * ldqk * 2));
   const u32x4_t rV = attn_rsrc(Vt, (uint32_t)((size_t)vt_rows * ldv * 2));
-  uint32_t kvo[4], vvo[4];
+  uint32_t kvo[J], vvo[J];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int row = 8 * (4 * wave + j) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+  for (int j = 0; j < J; j++) {
+    const int row = 8 * (J * wave + j) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
     kvo[j] = ((uint32_t)(base + row) * (uint32_t)ldqk + (uint32_t)(h * HD)) * 2u + (uint32_t)c * 16u;
     vvo[j] = ((uint32_t)(h * HD + row) * (uint32_t)ldv + (uint32_t)base) * 2u + (uint32_t)c * 16u;
   }
-  const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 4u * 1024u;
+  const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)J * 1024u;
   auto fetch_k = [&](int k0, u32x4_t* ks) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
+    for (int j = 0; j < J; j++) attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
   };
   auto fetch_v = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
+    for (int j = 0; j < J; j++) attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
   };
 
   f32x16_t o[2], lsum;
@@ -408,8 +418,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) st[kb][e] = __builtin_amdgcn_exp2f(fmaf(st[kb][e], c2, -mc));
-    // the running output and sum are rescaled only when some lane's max moved (alpha == 1 otherwise)
-    if (__any(m_new != m_run)) {
+    // the running output and sum are rescaled only when some valid query's max moved (alpha == 1
+    // otherwise, up to the rounding of m * c).  Lanes past the tile's last query stand in for its
+    // first query and do not vote, so the rescale points of a wave depend on its own queries only,
+    // whatever the tile size.
+    if (__any(qvalid && m_new != m_run)) {
       const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, -mc));
       lsum *= alpha;
 #pragma unroll
@@ -419,8 +432,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 
     // this block's V^T (fetched after the previous PV step, before the K fetch above) has landed
     // in every wave's part
-    if (more) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (more) {
+      if constexpr (J == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
@@ -470,12 +487,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
 
 template <typename T>
 void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt, int ldv, T* O, int ldo,
-                      const AttnTile* tiles, int ntiles, int H, const int* soff, const int* vlen, const int* gq,
-                      const int* grow, int window_half, float scale, hipStream_t st) {
+                      const AttnTile* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
+                      const int* gq, const int* grow, int window_half, float scale, hipStream_t st) {
   if (ntiles <= 0) return;
+  if (qtile != 64 && !(qtile == 128 && sizeof(T) == 2 && !gq)) {
+    fprintf(stderr, "[laya] attention: unsupported query tile %d\n", qtile);
+    abort();
+  }
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL(k_attention_bf16, dim3(H, ntiles), dim3(128), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O, ldo,
-                       tiles, soff, vlen, gq, grow, window_half, scale);
+    if (qtile == 128)
+      hipLaunchKernelGGL(k_attention_bf16<4>, dim3(H, ntiles), dim3(256), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
+                         ldo, tiles, soff, vlen, gq, grow, window_half, scale);
+    else
+      hipLaunchKernelGGL(k_attention_bf16<2>, dim3(H, ntiles), dim3(128), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
+                         ldo, tiles, soff, vlen, gq, grow, window_half, scale);
   } else {
     hipLaunchKernelGGL((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
                        vlen, gq, grow, window_half, scale);
@@ -483,10 +508,10 @@ void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt
 }
 
 template void launch_attention<float>(const float*, const float*, int, int, const float*, int, float*, int,
-                                      const AttnTile*, int, int, const int*, const int*, const int*, const int*, int,
-                                      float, hipStream_t);
+                                      const AttnTile*, int, int, int, const int*, const int*, const int*, const int*,
+                                      int, float, hipStream_t);
 template void launch_attention<bf16_t>(const bf16_t*, const bf16_t*, int, int, const bf16_t*, int, bf16_t*, int,
-                                       const AttnTile*, int, int, const int*, const int*, const int*, const int*, int,
-                                       float, hipStream_t);
+                                       const AttnTile*, int, int, int, const int*, const int*, const int*, const int*,
+                                       int, float, hipStream_t);
 
 }  // namespace laya

@@ -48,7 +48,7 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
       for (int j = 0; j < rows; j++) {
         p.ids[r + j] = j < len ? ids[ioff[b] + j] : pad_id; p.pos[r + j] = j; p.seq[r + j] = i;
       }
-      for (int q0 = 0; q0 < len; q0 += kQTile) p.tiles.push_back({i, q0, std::min(kQTile, len - q0), 0});
+      for (int q0 = 0; q0 < len; q0 += lim.q_tile) p.tiles.push_back({i, q0, std::min(lim.q_tile, len - q0), 0});
       r += rows; kt += nmark[b]; p.valid += len;
     }
     p.soff[n] = r;
@@ -84,7 +84,7 @@ PassCaps pass_caps(const PackLimits& lim) {
   PassCaps c;
   const int64_t rows = std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign));
   c.rows = rows;
-  c.tiles = rows / kQTile + lim.max_seqs;
+  c.tiles = rows / lim.q_tile + lim.max_seqs;
   c.grows = std::max(lim.max_grows, kMaxMarkers + 1);
   c.gtiles = c.grows / kQTile + lim.max_seqs;
   return c;

@@ -10,7 +10,8 @@
 //     them (pad token, positions continuing past len); padding rows are computed and never read,
 //     and every aligned group of kRowAlign rows belongs to one question, so the GEMM epilogue can
 //     write V^T [H][head_dim][rows] (column = row) with 16-byte stores;
-//   * attention work is a list of query tiles (seq, first query, query count) of <= 64 queries;
+//   * attention work is a list of query tiles (seq, first query, query count) of <= q_tile
+//     queries (64; 128 on request for the bf16 engine); gathered tiles hold <= 64 queries;
 //   * the last head layer works on R = KT + B gathered rows: the KT = sum(nmark) marker rows
 //     in question order, then one CLS row per question; gathered query tiles index a list of
 //     gathered-row ids.
@@ -21,7 +22,7 @@
 namespace laya {
 
 constexpr int kMaxMarkers = 255;     // options per question (the act head encodes k/255)
-constexpr int kQTile = 64;           // queries per attention tile
+constexpr int kQTile = 64;           // queries per gathered attention tile (and default encoder tile)
 constexpr int kRowAlign = 8;         // rows per aligned group (first row of every question)
 
 struct PackLimits {
@@ -31,6 +32,7 @@ struct PackLimits {
   int max_grows = 32768;             // gathered rows (sum of nmark + 1) per pass
   int vocab = 0;                     // > 0: ids must lie in [0, vocab)
   int pad_id = 0;                    // token id of padding rows
+  int q_tile = kQTile;               // queries per encoder / head-0 attention tile (64 or 128)
 };
 
 struct AttnTile { int32_t seq, q0, nq, pad; };

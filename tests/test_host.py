@@ -21,7 +21,7 @@ def host():
         build.build()
     L = ctypes.CDLL(le.HOST_LIB)
     IP = ctypes.POINTER(ctypes.c_int)
-    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 7 + [IP] * 7
+    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 8 + [IP] * 7
     L.laya_host_plan.restype = ctypes.c_int
     L.laya_host_config.argtypes = [ctypes.c_char_p, IP, ctypes.POINTER(ctypes.c_float), ctypes.c_char_p, ctypes.c_int]
     L.laya_host_config.restype = ctypes.c_int
@@ -38,9 +38,9 @@ def P(a):
 
 
 def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=512, max_grows=32768, vocab=0,
-         pad_id=0):
+         pad_id=0, q_tile=64):
     keep = [P(x if len(x) else [0]) for x in (lens, ids, nm, mk, qt)]
-    args = (max_len, pass_tokens, max_seqs, max_grows, vocab, pad_id)
+    args = (max_len, pass_tokens, max_seqs, max_grows, vocab, pad_id, q_tile)
     n = host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, -1, *([None] * 7))
     if n < 0:
         return None
@@ -83,12 +83,13 @@ def test_validation_minus_one(host):
     assert plan(host, [], [], [], [], []) == []                            # empty call: no pass
 
 
-def test_layout_of_a_pass(host):
+@pytest.mark.parametrize("q_tile", [64, 128])
+def test_layout_of_a_pass(host, q_tile):
     cfg = ck.PRESETS["tiny"]
-    b = wl.make_batch(cfg, [1, 64, 65, 200, 17], [1, 3, 255, 12, 2], seed=1)
-    (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id)
+    b = wl.make_batch(cfg, [1, 64, 65, 200, 17, 128, 129, 256], [1, 3, 255, 12, 2, 1, 4, 2], seed=1)
+    (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, q_tile=q_tile)
     rows8 = (b.lens + 7) // 8 * 8                                          # questions start on 8-row groups
-    assert p["B"] == 5 and p["T"] == int(rows8.sum()) and p["valid"] == int(b.lens.sum())
+    assert p["B"] == b.B and p["T"] == int(rows8.sum()) and p["valid"] == int(b.lens.sum())
     soff = np.concatenate([[0], np.cumsum(rows8)])
     assert np.array_equal(p["soff"], soff)
     for i in range(b.B):
@@ -98,10 +99,12 @@ def test_layout_of_a_pass(host):
         assert np.array_equal(p["pos"][r], np.arange(rows8[i]))
         assert np.all(p["seq"][r] == i)
         assert soff[i] % 8 == 0
-    # encoder tiles: every valid row of every question exactly once, <= 64 queries, inside its question
+    # encoder tiles: every valid row of every question exactly once, <= q_tile queries, inside its
+    # question, a full tile unless it holds the question's last row
     cover = np.zeros(p["T"], int)
     for seq, q0, nq, _ in p["tiles"]:
-        assert 1 <= nq <= 64 and q0 % 64 == 0 and q0 + nq <= b.lens[seq]
+        assert 1 <= nq <= q_tile and q0 % q_tile == 0 and q0 + nq <= b.lens[seq]
+        assert nq == q_tile or q0 + nq == b.lens[seq]
         cover[soff[seq] + q0: soff[seq] + q0 + nq] += 1
     valid_rows = np.concatenate([np.arange(soff[i], soff[i] + b.lens[i]) for i in range(b.B)])
     assert np.all(cover[valid_rows] == 1) and cover.sum() == p["valid"]
