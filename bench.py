@@ -16,8 +16,11 @@ roofline: per-stage device times come from HIP events on the engine's stream
 (laya_ext_prof_enable); the dominant kernel's achieved rate is its algorithmic work per launch
 (2*M*N*K flops for a GEMM over the valid tokens) divided by its average launch time.
 
-cpu_baseline: the CPU PyTorch restatement of the same forward pass (oracle/model.py, fp32) on
-the first questions of the same batch, on this host's cores.
+cpu_baseline: the CPU PyTorch restatement of the reference path (oracle/model.py, fp32 torch on
+this host's cores): the first questions of the same batch (about cpu-budget seconds), plus the
+median of five b1 x s128 ModernBERT-large forwards.  The restatement's speed relative to the
+reference's own CPU model was measured in the build container (tests/golden/large/cpu_timing.json)
+and is reported with it.
 """
 import argparse
 import json
@@ -37,6 +40,8 @@ PMC_COPY_BYTES = 256 << 20
 # calibrated HBM traffic per launch of the dominant kernel, from the committed rocprofv3 --pmc
 # summary (FETCH_SIZE and WRITE_SIZE runs of `bench.py --pmc-probe`, scaled by the copy kernel)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "c3_geglu_gemm_hbm_traffic.md")
+TRAFFIC_SOURCE = ("recorded, not measured in this run: profiles/c3_geglu_gemm_hbm_traffic.md (rocprofv3 --pmc "
+                  "FETCH_SIZE and WRITE_SIZE runs of bench.py --pmc-probe, copy-calibrated)")
 
 
 def measured_traffic(kernel_stage):
@@ -80,11 +85,34 @@ def attention_flops(lens, D, half_window):
     return {"global": 4.0 * D * s_glob, "sliding": 4.0 * D * s_slide}
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: this process's CPU share.  A GPU host gives each GPU's jobs a
+    share of its cores (OMP_NUM_THREADS says how many); os.cpu_count() counts the whole machine."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(avail, share) if share > 0 else avail)
+
+
 def cpu_baseline(cfg_name, batch, budget_s=20.0):
+    import statistics
     import torch
     from layamd_amd import checkpoint as ck
+    from layamd_amd import workloads as wl
     from oracle import model as om
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     cfg, W = ck.load_checkpoint(ck.cached_checkpoint(batch.cfg.name))
     Wt = om.Weights(W)
@@ -98,10 +126,35 @@ def cpu_baseline(cfg_name, batch, budget_s=20.0):
         n_tok += int(batch.lens[i])
         if time.time() - t0 > budget_s:
             break
-    return {"value": round(len(idx) / t_used, 4), "unit": "seqs/s", "cores": threads, "kind": "port",
-            "tokens_per_s": round(n_tok / t_used, 1),
-            "sample": "first %d of the %d questions (%d tokens), fp32 torch CPU restatement (oracle/model.py), "
-                      "one question per forward like the engine's packing" % (len(idx), batch.B, n_tok)}
+    # b1 x s128 ModernBERT-large, fp32: the configuration the reference's CPU path was timed on
+    c1 = wl.c1(0)
+    _, W1 = ck.load_checkpoint(ck.cached_checkpoint("large"))
+    W1t = om.Weights(W1)
+    ms = []
+    for r in range(2 + 5):
+        t = time.perf_counter()
+        om.run_batch(W1t, c1.cfg, c1)
+        if r >= 2:
+            ms.append(1e3 * (time.perf_counter() - t))
+    ratio = None
+    try:
+        with open(os.path.join(REPO, "tests", "golden", "large", "cpu_timing.json")) as f:
+            ratio = json.load(f)
+    except OSError:
+        pass
+    out = {"value": round(len(idx) / t_used, 4), "unit": "seqs/s", "cores": threads, "kind": "port",
+           "tokens_per_s": round(n_tok / t_used, 1),
+           "c1_b1s128_ms_median": round(statistics.median(ms), 2),
+           "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(), "cpu_model": cpu_model(),
+           "sample": "first %d of the %d questions (%d tokens) of %s, fp32 CPU PyTorch restatement of the reference "
+                     "path (oracle/model.py), one question per forward like the engine's packing, on %d threads (this "
+                     "process's CPU share; the host has %s logical CPUs); plus the median of 5 b1 x s128 forwards"
+                     % (len(idx), batch.B, n_tok, batch.name, threads, os.cpu_count())}
+    if ratio:
+        out["restatement_over_reference"] = ratio["restatement_over_reference"]
+        out["ratio_measured_on"] = "%s, %d threads, %s (reference DecisionModel %.1f ms, restatement %.1f ms at b1 x s128)" % (
+            ratio["cpu_model"], ratio["threads"], ratio["torch"], ratio["reference_ms_median"], ratio["restatement_ms_median"])
+    return out
 
 
 def main():
@@ -241,13 +294,15 @@ def main():
         ach = fl / (dom_ms * 1e-3) / 1e12
         peak = (PEAK_BF16 if elt == 2 else PEAK_FP32) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4), "traffic": measured_traffic(dom), "kernel": dom,
+                "frac": round(ach / peak, 4), "traffic": measured_traffic(dom), "traffic_source": TRAFFIC_SOURCE,
+                "kernel": dom,
                 "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T),
                 "achievable_peak": round(mfma_ach, 1), "frac_of_achievable": round(ach / mfma_ach, 4)}
     else:
         ach = by / (dom_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "kernel": dom,
+                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "traffic_source": TRAFFIC_SOURCE,
+                "kernel": dom,
                 "achievable_peak": round(copy_gbs, 1), "frac_of_achievable": round(ach / copy_gbs, 4)}
 
     cpu = None

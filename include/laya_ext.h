@@ -26,6 +26,25 @@ int laya_ext_replay(void* h, int iters, float* ms);
 /* "bf16" or "fp32": the storage type of GEMM and attention operands (LAYA_PRECISION). */
 const char* laya_ext_precision(void* h);
 
+/* Engine counters, the first n (<= 4) into out: [0] HIP graphs cached (one per pass bucket: rows
+ * and marker rows padded to 64, question count), [1] graphs captured so far, [2] tuned GEMM plans,
+ * [3] pass buckets whose GEMMs have been tuned.  Returns 0, or -1 for invalid arguments. */
+int laya_ext_stats(void* h, long long* out, int n);
+
+/* The engine's attention kernel on caller-owned device buffers, in the engine's packed layout:
+ * dtype 0 fp32 / 1 bf16 operands; Q and K [kv_rows][ldqk] (head h at columns 64 h .. 64 h + 63),
+ * V^T [H * 64][ldv] with column = packed row, O [..][ldo].  Question b owns rows soff[b] ..
+ * soff[b] + vlen[b] - 1 (soff a multiple of 8); V^T must hold 64 columns past the last row of
+ * every question.  tiles: ntiles x {question, first query, query count, 0} (int32; count 0 = skip),
+ * qtile 64 (or 128 for bf16 outside gathered mode).  Gathered mode when gq and grow are both
+ * non-NULL: tile queries are gathered rows gq[first + r], each the packed row grow[gq[...]], and
+ * their outputs go to row gq[...] of O.  window_half 0: every key of the question; otherwise keys
+ * with |i - j| <= window_half.  Launches on stream (hipStream_t) without waiting.  Returns 0, or
+ * -1 for arguments outside these rules. */
+int laya_ext_attention(int dtype, const void* Q, const void* K, int ldqk, int kv_rows, const void* Vt, int ldv, void* O,
+                       int ldo, const int* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
+                       const int* gq, const int* grow, int window_half, float scale, void* stream);
+
 /* The engine's MFMA GEMM on caller-owned device buffers: C[M,N] = A[M,K] . W[N,K]^T.
  * dtype 0: fp32 operands, 1: bf16 operands (fp32 accumulate in both).
  * epi 0: C (dtype) = act(result + bias), act 0 none / 1 ReLU / 2 GELU;
@@ -43,8 +62,8 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
  * achievable peak next to the published one.  Returns 0, or -1 for invalid arguments. */
 int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* flops);
 
-/* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 lets the planner
- * choose per GEMM (the default, or LAYA_GEMM_CFG); 0..8 select 256x256, 256x128, 128x256, 128x128,
+/* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 removes the pin
+ * (each engine's plans, or its own LAYA_GEMM_CFG read at laya_create, apply); 0..8 select 256x256, 256x128, 128x256, 128x128,
  * 192x256, 160x256, 128x192, 192x128 or 128x64 tiles (the QKV projection falls back to a shape that keeps its tiles inside one of
  * the q/k/v sections).  Passes already captured in HIP graphs keep their kernels.  Returns the
  * previous setting, or -2 for an invalid value. */

@@ -2,6 +2,8 @@
 
     layamd_amd/liblaya.so       the laya_api.h C ABI + gfx950 kernels (hipcc --offload-arch=gfx950)
     layamd_amd/liblaya_host.so  host-only packer/loader entry points for the CPU tests (g++)
+    layamd_amd/laya-parity      golden-format parity tool, a plain C++ caller of laya_api.h (g++)
+    layamd_amd/laya-bench       ABI latency tool (p50 per laya_forward_batch call), same (g++)
 
     python -m layamd_amd.build [--jobs N]
 
@@ -21,6 +23,7 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "liblaya.so")
 HOST_LIB = os.path.join(PKG, "liblaya_host.so")
+TOOLS = {"laya-parity": "laya_parity.cpp", "laya-bench": "laya_bench.cpp"}
 
 HIP_SOURCES = ["engine.hip", "kernels_gemm.hip", "kernels_attn.hip", "kernels_norm.hip"]
 CPP_SOURCES = ["model.cpp", "pack.cpp"]
@@ -72,8 +75,14 @@ def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
     _run(["g++"] + CXX_FLAGS + ["-shared", "-o", tmp, os.path.join(CSRC, "host_probe.cpp"),
                                 os.path.join(CSRC, "model.cpp"), os.path.join(CSRC, "pack.cpp")])
     os.replace(tmp, HOST_LIB)
+    # the C++ tools link the library like any C caller of laya_api.h would (found next to them)
+    for exe, src in TOOLS.items():
+        out = os.path.join(PKG, exe)
+        _run(["g++"] + CXX_FLAGS + ["-o", out + ".tmp", os.path.join(CSRC, "tools", src), "-L" + PKG, "-llaya",
+                                    "-Wl,-rpath,$ORIGIN"])
+        os.replace(out + ".tmp", out)
     if verbose:
-        print("[build] %s\n[build] %s" % (LIB, HOST_LIB))
+        print("[build] %s\n[build] %s\n[build] %s" % (LIB, HOST_LIB, ", ".join(os.path.join(PKG, e) for e in TOOLS)))
     return LIB
 
 

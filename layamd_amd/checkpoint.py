@@ -255,16 +255,31 @@ def read_safetensors(path: str) -> Dict[str, np.ndarray]:
     return out
 
 
-def checkpoint_id(c: ModelConfig, seed: int, std: float, ln_jitter: float, dtype: str) -> str:
-    h = hashlib.sha1(json.dumps([dataclasses.asdict(c), seed, std, ln_jitter, dtype]).encode()).hexdigest()[:10]
+def checkpoint_id(c: ModelConfig, seed: int, std: float, ln_jitter: float, dtype: str,
+                  round_to: Optional[str] = None) -> str:
+    key = [dataclasses.asdict(c), seed, std, ln_jitter, dtype] + ([round_to] if round_to else [])
+    h = hashlib.sha1(json.dumps(key).encode()).hexdigest()[:10]
     return "%s-s%d-%s" % (c.name, seed, h)
 
 
+def round_values(a: np.ndarray, round_to: Optional[str]) -> np.ndarray:
+    """float32 values rounded to the nearest BF16 or F16 value (None: unchanged)."""
+    if round_to == "BF16":
+        return bf16_bits_to_f32(to_bf16_bits(a)).reshape(a.shape)
+    if round_to == "F16":
+        return a.astype(np.float16).astype(np.float32)
+    if round_to is None:
+        return a
+    raise ValueError(round_to)
+
+
 def write_checkpoint(out_dir: str, c: ModelConfig, seed: int = 0, std: float = 0.02, ln_jitter: float = 0.0,
-                     dtype: str = "F32") -> str:
-    """Write a Laya model directory; skipped when a complete one with the same id exists."""
+                     dtype: str = "F32", round_to: Optional[str] = None) -> str:
+    """Write a Laya model directory; skipped when a complete one with the same id exists.  With
+    round_to ("BF16" or "F16") every value is first rounded to that type, so an F32 file can hold
+    exactly the weights of a BF16 or F16 file."""
     stamp = os.path.join(out_dir, "CHECKPOINT_ID")
-    cid = checkpoint_id(c, seed, std, ln_jitter, dtype)
+    cid = checkpoint_id(c, seed, std, ln_jitter, dtype, round_to)
     if os.path.exists(stamp) and open(stamp).read().strip() == cid:
         return out_dir
     os.makedirs(os.path.join(out_dir, "encoder"), exist_ok=True)
@@ -274,7 +289,8 @@ def write_checkpoint(out_dir: str, c: ModelConfig, seed: int = 0, std: float = 0
         json.dump(agent_config_json(c), f, indent=1)
     specs = tensor_specs(c)
     write_safetensors(os.path.join(out_dir, "model.safetensors"), [(n, s) for n, s, _ in specs],
-                      lambda i: gen_tensor(specs[i][2], specs[i][1], rng.stream_key(seed, i), std, ln_jitter),
+                      lambda i: round_values(gen_tensor(specs[i][2], specs[i][1], rng.stream_key(seed, i), std,
+                                                        ln_jitter), round_to),
                       dtype)
     with open(stamp, "w") as f:
         f.write(cid + "\n")
@@ -317,8 +333,9 @@ def cache_root() -> str:
     return os.environ.get("LAYA_CKPT_CACHE", os.path.join(tempfile.gettempdir(), "laya_ckpt"))
 
 
-def cached_checkpoint(preset: str, seed: int = 0, std: float = 0.02, ln_jitter: float = 0.0, dtype: str = "F32") -> str:
+def cached_checkpoint(preset: str, seed: int = 0, std: float = 0.02, ln_jitter: float = 0.0, dtype: str = "F32",
+                      round_to: Optional[str] = None) -> str:
     """Seeded checkpoint of a preset under $LAYA_CKPT_CACHE (default /tmp/laya_ckpt), written once."""
     c = PRESETS[preset]
-    d = os.path.join(cache_root(), checkpoint_id(c, seed, std, ln_jitter, dtype))
-    return write_checkpoint(d, c, seed=seed, std=std, ln_jitter=ln_jitter, dtype=dtype)
+    d = os.path.join(cache_root(), checkpoint_id(c, seed, std, ln_jitter, dtype, round_to))
+    return write_checkpoint(d, c, seed=seed, std=std, ln_jitter=ln_jitter, dtype=dtype, round_to=round_to)

@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -92,6 +93,8 @@ struct EngineIface {
   virtual void warmup() = 0;
   virtual void tune_all() = 0;
   virtual const char* precision() const = 0;
+  // graphs cached, graphs captured so far, tuned GEMM plans, pass buckets tuned
+  virtual void stats(long long* out) const = 0;
 };
 
 template <typename T>
@@ -129,13 +132,19 @@ struct Engine : EngineIface {
   size_t blob_cap = 0;
   float *h_logits, *h_act;
 
+  // A pass bucket: rows (a multiple of kRowBucket), questions, marker rows (a multiple of
+  // kMarkerBucket).  Everything a pass launches and every index array's size follow from it: the
+  // gathered rows R = KT + B and the attention grids (the tile capacities of pack.h).
   struct Shape {
-    int rows, B, KT, R, nt, ngt;
-    bool operator<(const Shape& o) const {
-      return std::tie(rows, B, KT, R, nt, ngt) < std::tie(o.rows, o.B, o.KT, o.R, o.nt, o.ngt);
-    }
+    int rows, B, KT;
+    int R() const { return KT + B; }
+    int nt() const { return tiles_cap(rows, B); }
+    int ngt() const { return gtiles_cap(R(), B); }
+    bool operator<(const Shape& o) const { return std::tie(rows, B, KT) < std::tie(o.rows, o.B, o.KT); }
   };
   std::map<Shape, hipGraphExec_t> graphs;
+  size_t max_graphs = 512;                // the reference's cache limit (src/engine.hip:477)
+  long long n_captures = 0;               // graphs captured so far (cache misses that were captured)
   bool have_last = false;
   Shape last{};
 
@@ -149,9 +158,16 @@ struct Engine : EngineIface {
   int n_cu = 256;
   std::set<Shape> tuned_shapes;
   bool tune_on = true;
+  // LAYA_GEMM_CFG / LAYA_GEMM_SPLIT, read at laya_create: one tile configuration (and row split)
+  // for every bf16 GEMM of this engine instead of the tuned plans
+  int pin_cfg = -1, pin_split = 0, pin_tail = -1;
   std::vector<std::pair<int, GemmArgs>>* collecting = nullptr;   // set while a pass's GEMMs are listed
 
   const char* precision() const override { return sizeof(T) == 2 ? "bf16" : "fp32"; }
+  void stats(long long* out) const override {
+    out[0] = (long long)graphs.size(); out[1] = n_captures; out[2] = (long long)tuned.size();
+    out[3] = (long long)tuned_shapes.size();
+  }
 
   // ------------------------------------------------------------ allocation helpers
   template <typename U> U* dalloc(size_t n, bool zero = false) {
@@ -310,6 +326,13 @@ struct Engine : EngineIface {
     // attention query tiles: 64 queries (two waves in bf16); LAYA_ATTN_QTILE=128 gives bf16 128-query
     // tiles of four waves, same bits, measured slower on sliding-window layers
     lim.q_tile = sizeof(T) == 2 && env_int("LAYA_ATTN_QTILE", 64) == 128 ? 128 : 64;
+    if (lim.q_tile == 128 && (cfg.local_attention / 2) % 64 != 0) {
+      // 128-query tiles visit the same key blocks as 64-query tiles only when the sliding window's
+      // half width is a multiple of 64 (both tilings then start every query's keys on the same
+      // 64-key boundaries); otherwise the tiling would change the bits
+      fprintf(stderr, "[laya] LAYA_ATTN_QTILE=128 needs local_attention / 2 to be a multiple of 64; using 64\n");
+      lim.q_tile = 64;
+    }
     caps = pass_caps(lim);
     MT = caps.rows; RG = caps.grows; VTC = (MT + 64 + 63) / 64 * 64;
     x = dalloc<float>((size_t)MT * D);
@@ -319,7 +342,9 @@ struct Engine : EngineIface {
     mg = dalloc<T>((size_t)MT * I);
     ff = dalloc<T>((size_t)std::max(MT, RG) * FF);
     xg = dalloc<float>((size_t)RG * D);
-    aog = dalloc<T>((size_t)RG * D); xng = dalloc<T>((size_t)RG * D); sh = dalloc<T>((size_t)RG * D);
+    // the gathered buffers are zeroed once: rows past a pass's gathered queries (the marker padding)
+    // are read by the row-wise head GEMMs, which must see finite values
+    aog = dalloc<T>((size_t)RG * D, true); xng = dalloc<T>((size_t)RG * D, true); sh = dalloc<T>((size_t)RG * D, true);
     if (sizeof(T) == 2) sk_ws = dalloc<float>(kSplitKBytes / sizeof(float));
     d_logits = dalloc<float>((size_t)RG);
     d_act = dalloc<float>((size_t)lim.max_seqs * cfg.n_act);
@@ -327,12 +352,11 @@ struct Engine : EngineIface {
     h_logits = halloc<float>((size_t)RG);
     h_act = halloc<float>((size_t)lim.max_seqs * cfg.n_act);
     {
-      const Shape cap{(int)MT, lim.max_seqs, (int)RG, (int)RG, (int)caps.tiles, (int)caps.gtiles};
-      blob_cap = blob_layout(cap).total;
-      d_blob = dalloc<char>(blob_cap);
+      blob_cap = blob_layout((int)MT, caps.seqs, (int)RG, (int)caps.tiles, (int)caps.gtiles).total;
+      d_blob = dalloc<char>(blob_cap, true);
       h_blob = halloc<char>(blob_cap);
       memset(h_blob, 0, blob_cap);
-      bind(cap);
+      bind(Shape{(int)MT, 1, 0});
     }
 
     LAYA_HIP(hipStreamCreate(&stream));
@@ -343,7 +367,18 @@ struct Engine : EngineIface {
     }
     prof.init();
     use_graphs = env_int("LAYA_GRAPHS", 1) != 0;
+    max_graphs = (size_t)std::max(0, env_int("LAYA_MAX_GRAPHS", 512));
     tune_on = env_int("LAYA_TUNE", 1) != 0;
+    if (const char* e = getenv("LAYA_GEMM_CFG")) {
+      pin_cfg = atoi(e);
+      if (pin_cfg < 0 || pin_cfg >= kGemmConfigs) pin_cfg = -1;
+      int rows = 0, tail = -1;
+      const char* sp = getenv("LAYA_GEMM_SPLIT");
+      if (pin_cfg >= 0 && sp && sscanf(sp, "%d,%d", &rows, &tail) == 2 && rows > 0 && tail >= 0 && tail < kGemmConfigs) {
+        pin_split = rows;
+        pin_tail = tail;
+      }
+    }
     dump_dir = getenv("LAYA_DUMP_DIR");
     if (dump_dir && !*dump_dir) dump_dir = nullptr;
     LAYA_HIP(hipDeviceSynchronize());
@@ -352,20 +387,21 @@ struct Engine : EngineIface {
   }
 
   // ------------------------------------------------------------ one pass
-  // byte offsets of the index arrays of a pass shape in the blocks (256-byte aligned)
+  // byte offsets of the index arrays of a pass bucket in the blocks (256-byte aligned)
   struct BlobLayout { size_t ids, pos, seq, soff, vlen, qt, nm, moff, gq, grow, tiles, gtiles, total; };
-  static BlobLayout blob_layout(const Shape& s) {
+  static BlobLayout blob_layout(int rows, int B, int R, int nt, int ngt) {
     BlobLayout L;
     size_t o = 0;
     auto take = [&](size_t bytes) { const size_t r = o; o += (bytes + 255) & ~(size_t)255; return r; };
-    L.ids = take((size_t)s.rows * 4); L.pos = take((size_t)s.rows * 4); L.seq = take((size_t)s.rows * 4);
-    L.soff = take((size_t)(s.B + 1) * 4); L.vlen = take((size_t)s.B * 4); L.qt = take((size_t)s.B * 4);
-    L.nm = take((size_t)s.B * 4); L.moff = take((size_t)s.B * 4);
-    L.gq = take((size_t)s.R * 4); L.grow = take((size_t)s.R * 4);
-    L.tiles = take((size_t)s.nt * sizeof(AttnTile)); L.gtiles = take((size_t)s.ngt * sizeof(AttnTile));
+    L.ids = take((size_t)rows * 4); L.pos = take((size_t)rows * 4); L.seq = take((size_t)rows * 4);
+    L.soff = take((size_t)(B + 1) * 4); L.vlen = take((size_t)B * 4); L.qt = take((size_t)B * 4);
+    L.nm = take((size_t)B * 4); L.moff = take((size_t)B * 4);
+    L.gq = take((size_t)R * 4); L.grow = take((size_t)R * 4);
+    L.tiles = take((size_t)nt * sizeof(AttnTile)); L.gtiles = take((size_t)ngt * sizeof(AttnTile));
     L.total = o;
     return L;
   }
+  static BlobLayout blob_layout(const Shape& s) { return blob_layout(s.rows, s.B, s.R(), s.nt(), s.ngt()); }
   void bind(const Shape& s) {
     const BlobLayout L = blob_layout(s);
     auto at = [&](size_t off, int** d, int** h) { *d = (int*)(d_blob + off); *h = (int*)(h_blob + off); };
@@ -377,6 +413,11 @@ struct Engine : EngineIface {
   }
 
   void stage_inputs(const PassPlan& p) {
+    const Shape s{p.T, p.B, p.KT};
+    if ((int)p.tiles.size() != s.nt() || (int)p.gtiles.size() != s.ngt() || p.R != s.R() || (int)p.gq.size() > p.R) {
+      fprintf(stderr, "[laya] internal error: pass arrays do not match their bucket\n");
+      exit(1);
+    }
     memcpy(h_ids, p.ids.data(), p.T * 4); memcpy(h_pos, p.pos.data(), p.T * 4);
     memcpy(h_seq, p.seq.data(), p.T * 4);
     memcpy(h_soff, p.soff.data(), (p.B + 1) * 4); memcpy(h_vlen, p.vlen.data(), p.B * 4);
@@ -416,10 +457,12 @@ struct Engine : EngineIface {
   }
 
   // ------------------------------------------------------------ GEMM tile tuning
-  // M buckets: multiples of 64 rows up to 1024, then 32 buckets per octave
+  // M buckets: multiples of 64 rows up to 1024, then 16 buckets per octave up to 8192 rows and 8
+  // per octave above (88 buckets up to 65536 rows); every bucket bound is a multiple of 64
   static int m_bucket(int M) {
     if (M <= 1024) return (M + 63) / 64 * 64;
-    const int step = 1 << (31 - __builtin_clz((unsigned)M) - 5);
+    const int lg = 31 - __builtin_clz((unsigned)(M - 1));          // 2^lg < M <= 2^(lg + 1)
+    const int step = (1 << lg) / (lg < 13 ? 16 : 8);
     return (M + step - 1) / step * step;
   }
   static TuneKey tune_key(int epi, const GemmArgs& g) {
@@ -430,8 +473,12 @@ struct Engine : EngineIface {
   // the measured configuration of its bucket (the analytic planner's where none was measured)
   void gemm(int epi, GemmArgs g, hipStream_t st) {
     if (collecting) { collecting->emplace_back(epi, g); return; }
-    auto it = tuned.find(tune_key(epi, g));
-    if (it != tuned.end()) apply_plan(g, it->second);
+    if (pin_cfg >= 0) {
+      g.cfg = pin_cfg; g.split_rows = pin_split; g.cfg_tail = pin_tail;
+    } else {
+      auto it = tuned.find(tune_key(epi, g));
+      if (it != tuned.end()) apply_plan(g, it->second);
+    }
     launch_gemm<T>(epi, g, st);
   }
 
@@ -505,7 +552,7 @@ struct Engine : EngineIface {
   // lists the GEMMs of pass shape s (uploading its index arrays, which the QKV epilogue reads) and
   // tunes the buckets not yet measured
   void tune_pass(const Shape& s) {
-    if (!tune_on || sizeof(T) != 2 || gemm_pinned() >= 0 || capturing || tuned_shapes.count(s)) return;
+    if (!tune_on || sizeof(T) != 2 || gemm_pinned() >= 0 || pin_cfg >= 0 || capturing || tuned_shapes.count(s)) return;
     std::vector<std::pair<int, GemmArgs>> list;
     collecting = &list;
     run(s);
@@ -521,13 +568,14 @@ struct Engine : EngineIface {
   // every M bucket up to the pass capacity, for every GEMM of the model (the gathered head rows and
   // the scorer share the encoder's and head's (N, K) shapes at other M)
   void tune_all() override {
-    if (tune_on && sizeof(T) == 2 && gemm_pinned() < 0) {
+    if (tune_on && sizeof(T) == 2 && gemm_pinned() < 0 && pin_cfg < 0) {
       // the listing run uploads the host block: all zeros (position 0) keeps the RoPE table reads
-      // in range whatever the layout
+      // in range whatever the layout.  The gathered-row GEMMs (KT + 1 rows) and the scorer (KT rows)
+      // are listed at the largest marker bucket below the row bucket.
       memset(h_blob, 0, blob_cap);
       for (int mb = 64; mb <= MT; mb = m_bucket(mb + 1)) {
-        const int r = (int)std::min<int64_t>(mb, RG);
-        tune_pass(Shape{mb, 1, r - 1, r, 0, 0});
+        const int kt = (int)std::max<int64_t>(kMarkerBucket, std::min<int64_t>(mb, RG - 1) / kMarkerBucket * kMarkerBucket);
+        tune_pass(Shape{mb, 1, kt});
       }
     }
     warmup();
@@ -536,7 +584,7 @@ struct Engine : EngineIface {
   void run(const Shape& s) {
     const int D = cfg.d, H = cfg.n_heads, HD = cfg.head_dim, I = cfg.intermediate, FF = cfg.head_ffn;
     const float eps = cfg.norm_eps, scale = 1.0f / sqrtf((float)HD);
-    const int T_ = s.rows, B = s.B, KT = s.KT, R = s.R;
+    const int T_ = s.rows, B = s.B, KT = s.KT, R = s.R();
     hipStream_t st = stream;
     auto h2d = [&](void* d, const void* h, size_t n) { LAYA_HIP(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st)); };
     bind(s);
@@ -561,7 +609,7 @@ struct Engine : EngineIface {
         GSTAGE("enc:gemm_qkv_rope", gemm(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
-            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, lim.q_tile, H, d_soff, d_vlen,
+            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt(), lim.q_tile, H, d_soff, d_vlen,
                                 nullptr, nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
@@ -603,7 +651,7 @@ struct Engine : EngineIface {
         GSTAGE("head:gemm_qkv", gemm(EPI_QKV, g, st));
       }
       if (!last) {
-        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt, lim.q_tile, H, d_soff,
+        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt(), lim.q_tile, H, d_soff,
                                                d_vlen, nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
@@ -616,7 +664,7 @@ struct Engine : EngineIface {
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
-        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt, kQTile, H, d_soff,
+        STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt(), kQTile, H, d_soff,
                                                         d_vlen, d_gq, d_grow, 0, scale, st));
         STAGE("head:gather", launch_gather_rows(x, d_grow, xg, R, D, st));
         { GemmArgs g = gemm_args(aog, D, hl.outW, R, D, D, hl.outB); g.X = xg; g.ldx = D; splitk(g);
@@ -660,7 +708,7 @@ struct Engine : EngineIface {
     tune_pass(s);
     run(s);
     LAYA_HIP(hipStreamSynchronize(stream));
-    if (!graphs_on || graphs.size() >= 512) return;
+    if (!graphs_on || graphs.size() >= max_graphs) return;
     hipGraph_t g;
     hipGraphExec_t ex;
     if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { use_graphs = false; return; }
@@ -675,6 +723,7 @@ struct Engine : EngineIface {
     }
     LAYA_HIP(hipGraphDestroy(g));
     graphs[s] = ex;
+    n_captures++;
   }
 
   int forward_batch(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
@@ -684,7 +733,7 @@ struct Engine : EngineIface {
     std::vector<int64_t> moff(B + 1, 0);
     for (int b = 0; b < B; b++) moff[b + 1] = moff[b] + nmark[b];
     for (const PassPlan& p : passes) {
-      Shape s{p.T, p.B, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size()};
+      const Shape s{p.T, p.B, p.KT};
       bind(s);
       stage_inputs(p);
       execute(s);
@@ -819,6 +868,40 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
   return 0;
 }
 const char* laya_ext_precision(void* h) { return E(h)->precision(); }
+
+int laya_ext_stats(void* h, long long* out, int n) {
+  if (!h || !out || n < 1) return -1;
+  long long v[4];
+  E(h)->stats(v);
+  for (int i = 0; i < n && i < 4; i++) out[i] = v[i];
+  return 0;
+}
+
+int laya_ext_attention(int dtype, const void* Q, const void* K, int ldqk, int kv_rows, const void* Vt, int ldv, void* O,
+                       int ldo, const int* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
+                       const int* gq, const int* grow, int window_half, float scale, void* stream) {
+  using namespace laya;
+  const int elt = dtype == 0 ? 4 : 2;
+  if ((dtype != 0 && dtype != 1) || !Q || !K || !Vt || !O || !tiles || !soff || !vlen || ntiles < 0 || H < 1 ||
+      kv_rows < 1 || window_half < 0 || !(scale > 0.f) || (gq == nullptr) != (grow == nullptr))
+    return -1;
+  if (qtile != 64 && !(qtile == 128 && dtype == 1 && !gq)) return -1;
+  if (ldqk < H * 64 || ldo < H * 64 || ldv < 64 || (ldqk * elt) % 16 || (ldo * elt) % 16 || (ldv * elt) % 16) return -1;
+  if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(Vt) |
+       reinterpret_cast<uintptr_t>(O)) & 15)
+    return -1;
+  hipStream_t st = (hipStream_t)stream;
+  (void)hipGetLastError();
+  const AttnTile* t = reinterpret_cast<const AttnTile*>(tiles);
+  if (dtype == 0)
+    launch_attention<float>((const float*)Q, (const float*)K, ldqk, kv_rows, (const float*)Vt, ldv, (float*)O, ldo, t,
+                            ntiles, qtile, H, soff, vlen, gq, grow, window_half, scale, st);
+  else
+    launch_attention<bf16_t>((const bf16_t*)Q, (const bf16_t*)K, ldqk, kv_rows, (const bf16_t*)Vt, ldv, (bf16_t*)O, ldo,
+                             t, ntiles, qtile, H, soff, vlen, gq, grow, window_half, scale, st);
+  LAYA_HIP(hipGetLastError());
+  return 0;
+}
 int laya_ext_gemm_ksplit(int ks, void* ws, size_t ws_bytes) {
   if (ks < 0 || ks > 64 || (ks > 1 && (!ws || ws_bytes == 0))) return -2;
   g_ext_ws = static_cast<float*>(ws);

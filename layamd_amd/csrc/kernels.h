@@ -57,7 +57,8 @@ struct GemmArgs {
 template <typename T>
 void launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why);
-// pins the bf16 tile configuration for later launches (-1: the planner; 0..8: 256x256, 256x128,
+// pins the bf16 tile configuration for later launches, process-wide (-1: none, the caller's or the
+// planner's choice; 0..8: 256x256, 256x128,
 // 128x256, 128x128, 192x256, 160x256, 128x192, 192x128, 128x64); returns the previous setting
 int gemm_config(int cfg);
 int gemm_pinned();                               // the pinned configuration, or -1
@@ -86,7 +87,8 @@ int gemm_planned(int epi, const GemmArgs& a);
 // grow[gq[tile.q0 + r]], outputs go to row gq[...] of O).  window_half = 0: all keys of the
 // sequence; otherwise keys with |i - j| <= window_half.  V^T column = packed row; sequences start
 // on 8-row boundaries and V^T has 64 columns of slack after the last row.  Q and K hold kv_rows
-// rows; V^T has H * 64 rows.
+// rows; V^T has H * 64 rows.  Tiles with nq = 0 are skipped (a pass pads its tile list to a
+// capacity that depends only on its bucket).
 template <typename T>
 void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt, int ldv, T* O, int ldo,
                       const AttnTile* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,

@@ -44,6 +44,7 @@ __global__ __launch_bounds__(256) void k_attention(const T* __restrict__ Q, cons
   __shared__ u32x4_t Vs[64 * CPR];                       // [d][...] swizzled by d
 
   const AttnTile tile = tiles[blockIdx.x];
+  if (tile.nq <= 0) return;                              // an empty tile of the pass's tile capacity
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
   const int b = tile.seq, len = vlen[b], base = soff[b], vb = base;   // V^T column = row
@@ -245,12 +246,12 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 // ======================================================================================
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// LDS DMA of one 16-byte chunk per lane (see the GEMM's dma16: M0 is the LDS base, the whole
-// offset is range-checked, the memory clobber orders it against LDS reads)
+// LDS DMA of one 16-byte chunk per lane (see the GEMM's dma16: the LDS base is an operand bound
+// to M0, the whole offset is range-checked, the memory clobber orders it against LDS reads)
 __device__ __forceinline__ void attn_dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(rsrc)
+               : "{m0}"(lds), "v"(voff), "s"(rsrc)
                : "memory");
 }
 
@@ -285,6 +286,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 
   // heads are the fastest grid dimension, so the (longest-first) tiles start in order
   const AttnTile tile = tiles[blockIdx.y];
+  if (tile.nq <= 0) return;                               // an empty tile of the pass's tile capacity
   const int h = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
   const int b = tile.seq, len = vlen[b], base = soff[b];

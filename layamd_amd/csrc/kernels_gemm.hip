@@ -316,15 +316,15 @@ __device__ __forceinline__ u32x4_t make_rsrc(const void* p, uint32_t bytes) {
 }
 
 // One LDS DMA instruction: lane l copies 16 bytes at rsrc + voff + soff to LDS address lds + 16 l.
-// Issued as inline assembly (M0 holds the LDS base; one wait state between the M0 write and the
-// DMA; no compiler-generated code in these kernels reads M0, which gfx9 LDS instructions ignore),
-// so the compiler sees no LDS write and inserts no waits of its own between these fills and the
-// fragment reads: the main loop orders them with explicit vmcnt waits and barriers.  The memory
-// clobber keeps the compiler from moving LDS reads across the fill.
+// Issued as inline assembly, so the compiler sees no LDS write and inserts no waits of its own
+// between these fills and the fragment reads: the main loop orders them with explicit vmcnt waits
+// and barriers.  The LDS base is an operand bound to M0 ("{m0}"), so the compiler writes M0 itself
+// and knows the instruction reads it; the asm adds one wait state between that write and the DMA.
+// The memory clobber keeps the compiler from moving LDS reads across the fill.
 __device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "{m0}"(lds), "v"(voff), "s"(rsrc), "s"(soff)
                : "memory");
 }
 
@@ -1155,30 +1155,15 @@ static const XlCfg kXl[kGemmConfigs] = {{256, 256, 1, 1.00f}, {256, 128, 1, 0.80
                                         {128, 128, 2, 0.72f}, {192, 256, 1, 0.95f}, {160, 256, 1, 0.93f},
                                         {128, 192, 2, 0.80f}, {192, 128, 2, 0.80f}, {128, 64, 2, 0.50f}};
 
-// tile configuration pinned for every bf16 launch (-1: none); LAYA_GEMM_CFG sets it at the first
-// launch, gemm_config() at run time
-static std::atomic<int> g_gemm_cfg{-2};
+// tile configuration pinned for every bf16 launch, process-wide (-1: none), by gemm_config()
+// (laya_ext_gemm_config); an engine's LAYA_GEMM_CFG is that engine's own and reaches the launches
+// as the caller's configuration
+static std::atomic<int> g_gemm_cfg{-1};
 
 // row split applied with the pinned configuration (0: none)
 static std::atomic<int> g_split_rows{0}, g_cfg_tail{-1};
 
-int gemm_pinned() {
-  int v = g_gemm_cfg.load(std::memory_order_relaxed);
-  if (v == -2) {
-    const char* e = getenv("LAYA_GEMM_CFG");
-    v = e ? atoi(e) : -1;
-    if (v < -1 || v >= kGemmConfigs) v = -1;
-    // LAYA_GEMM_SPLIT=rows,cfg: with a pinned configuration, rows [rows, M) in a second launch
-    const char* sp = getenv("LAYA_GEMM_SPLIT");
-    int rows = 0, tail = -1;
-    if (v >= 0 && sp && sscanf(sp, "%d,%d", &rows, &tail) == 2 && rows > 0 && tail >= 0 && tail < kGemmConfigs) {
-      g_split_rows.store(rows, std::memory_order_relaxed);
-      g_cfg_tail.store(tail, std::memory_order_relaxed);
-    }
-    g_gemm_cfg.store(v, std::memory_order_relaxed);
-  }
-  return v;
-}
+int gemm_pinned() { return g_gemm_cfg.load(std::memory_order_relaxed); }
 
 int gemm_config(int cfg) {
   const int prev = gemm_pinned();
@@ -1379,8 +1364,8 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
         launch_splitk(epi, a, ks, st);
         return;
       }
-      // a pinned configuration (LAYA_GEMM_CFG / gemm_config, with its pinned row split) wins over
-      // the caller's, which wins over the planner's; one this shape cannot use falls through
+      // a pinned configuration (gemm_config, with its pinned row split) wins over the caller's,
+      // which wins over the planner's; one this shape cannot use falls through
       int cfg = a.cfg, split = a.split_rows, tail = a.cfg_tail;
       const int pinned = gemm_pinned();
       if (xl_cfg_fits(epi, a, pinned)) {

@@ -30,38 +30,44 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
       }
   }
   const int pass_rows = std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign));
+  const int grows_cap = std::max(lim.max_grows, align_up(kMaxMarkers, kMarkerBucket) + 1);
   int b0 = 0;
   while (b0 < B) {
-    int n = 0, T = 0, R = 0;
+    int n = 0, T = 0, kt = 0;
+    // questions in order while the rows fit the pass and the gathered rows (markers padded to
+    // their bucket, plus one CLS row per question) fit the gathered buffers
     while (b0 + n < B && n < lim.max_seqs && T + align_up(lens[b0 + n], kRowAlign) <= pass_rows &&
-           R + nmark[b0 + n] + 1 <= std::max(lim.max_grows, kMaxMarkers + 1)) {
-      T += align_up(lens[b0 + n], kRowAlign); R += nmark[b0 + n] + 1; n++;
+           align_up(kt + nmark[b0 + n], kMarkerBucket) + n + 1 <= grows_cap) {
+      T += align_up(lens[b0 + n], kRowAlign); kt += nmark[b0 + n]; n++;
     }
     PassPlan p;
-    p.first = b0; p.B = n; p.T = T;
-    p.ids.resize(T); p.pos.resize(T); p.seq.resize(T);
+    p.first = b0; p.B = n; p.T = align_up(T, kRowBucket);
+    p.markers = kt;
+    p.KT = align_up(kt, kMarkerBucket);
+    p.R = p.KT + n;
+    p.ids.resize(p.T); p.pos.resize(p.T); p.seq.resize(p.T);
     p.soff.resize(n + 1); p.vlen.resize(n); p.qt.resize(n); p.nm.resize(n); p.moff.resize(n);
-    int r = 0, kt = 0;
+    int r = 0, mo = 0;
     for (int i = 0; i < n; i++) {
       const int b = b0 + i, len = lens[b], rows = align_up(len, kRowAlign);
-      p.soff[i] = r; p.vlen[i] = len; p.qt[i] = qtypes[b]; p.nm[i] = nmark[b]; p.moff[i] = kt;
+      p.soff[i] = r; p.vlen[i] = len; p.qt[i] = qtypes[b]; p.nm[i] = nmark[b]; p.moff[i] = mo;
       for (int j = 0; j < rows; j++) {
         p.ids[r + j] = j < len ? ids[ioff[b] + j] : pad_id; p.pos[r + j] = j; p.seq[r + j] = i;
       }
       for (int q0 = 0; q0 < len; q0 += lim.q_tile) p.tiles.push_back({i, q0, std::min(lim.q_tile, len - q0), 0});
-      r += rows; kt += nmark[b]; p.valid += len;
+      r += rows; mo += nmark[b]; p.valid += len;
     }
     p.soff[n] = r;
-    p.KT = kt; p.R = kt + n;
-    p.grow.resize(p.R);
+    for (int j = r; j < p.T; j++) { p.ids[j] = pad_id; p.pos[j] = 0; p.seq[j] = n - 1; }   // the bucket's tail rows
+    p.grow.assign(p.R, 0);                                 // marker padding: row 0, computed, never read
     for (int i = 0; i < n; i++) {
       const int b = b0 + i;
       for (int k = 0; k < nmark[b]; k++) p.grow[p.moff[i] + k] = p.soff[i] + markers[moff[b] + k];
-      p.grow[kt + i] = p.soff[i];                          // CLS row
+      p.grow[p.KT + i] = p.soff[i];                        // CLS row
       // this question's gathered queries: its markers, then its CLS row
       std::vector<int32_t> q;
       for (int k = 0; k < nmark[b]; k++) q.push_back(p.moff[i] + k);
-      q.push_back(kt + i);
+      q.push_back(p.KT + i);
       for (size_t s = 0; s < q.size(); s += kQTile) {
         int cnt = (int)std::min<size_t>(kQTile, q.size() - s);
         p.gtiles.push_back({i, (int)p.gq.size(), cnt, 0});
@@ -74,6 +80,9 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
     auto by_len = [&](const AttnTile& x, const AttnTile& y) { return p.vlen[x.seq] > p.vlen[y.seq]; };
     std::stable_sort(p.tiles.begin(), p.tiles.end(), by_len);
     std::stable_sort(p.gtiles.begin(), p.gtiles.end(), by_len);
+    // empty tiles up to the bucket's capacities (the launch grids)
+    p.tiles.resize(tiles_cap(p.T, n), AttnTile{0, 0, 0, 0});
+    p.gtiles.resize(gtiles_cap(p.R, n), AttnTile{0, 0, 0, 0});
     passes->push_back(std::move(p));
     b0 += n;
   }
@@ -82,11 +91,11 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
 
 PassCaps pass_caps(const PackLimits& lim) {
   PassCaps c;
-  const int64_t rows = std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign));
-  c.rows = rows;
-  c.tiles = rows / lim.q_tile + lim.max_seqs;
-  c.grows = std::max(lim.max_grows, kMaxMarkers + 1);
-  c.gtiles = c.grows / kQTile + lim.max_seqs;
+  c.rows = align_up(std::max(lim.pass_tokens, align_up(lim.max_len, kRowAlign)), kRowBucket);
+  c.seqs = std::max(1, lim.max_seqs);
+  c.grows = std::max(lim.max_grows, align_up(kMaxMarkers, kMarkerBucket) + 1);
+  c.tiles = tiles_cap((int)c.rows, c.seqs);
+  c.gtiles = gtiles_cap((int)c.grows, c.seqs);
   return c;
 }
 

@@ -12,10 +12,8 @@ a missing library raises.
 """
 import ctypes
 import importlib.util
-import itertools
 import os
 import sys
-from array import array
 from typing import List, Optional
 
 import numpy as np
@@ -27,7 +25,13 @@ HOST_LIB = os.path.join(PKG, "liblaya_host.so")
 ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act", "laya_max_len",
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
-               "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop"]
+               "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop",
+               "laya_ext_stats", "laya_ext_attention"]
+# every environment variable laya_create reads; Engine() sets the ones it is given for the duration
+# of laya_create only
+ENV_KNOBS = ["LAYA_PRECISION", "LAYA_MAX_TOKENS", "LAYA_PASS_TOKENS", "LAYA_MAX_SEQS", "LAYA_MAX_GATHERED",
+             "LAYA_ATTN_QTILE", "LAYA_GRAPHS", "LAYA_MAX_GRAPHS", "LAYA_TUNE", "LAYA_GEMM_CFG", "LAYA_GEMM_SPLIT",
+             "LAYA_PROFILE", "LAYA_DUMP_DIR", "LAYA_VERBOSE"]
 
 _IP = ctypes.POINTER(ctypes.c_int)
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -89,6 +93,12 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.POINTER(ctypes.c_double)]
     L.laya_ext_mfma_loop.restype = ctypes.c_int
+    L.laya_ext_stats.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_longlong), ctypes.c_int]
+    L.laya_ext_stats.restype = ctypes.c_int
+    L.laya_ext_attention.argtypes = ([ctypes.c_int] + [ctypes.c_void_p] * 2 + [ctypes.c_int] * 2 + [ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
+    L.laya_ext_attention.restype = ctypes.c_int
     return L
 
 
@@ -156,19 +166,46 @@ def _ptr(a: np.ndarray, ct):
     return a.ctypes.data_as(ctypes.POINTER(ct))
 
 
+def attention(lib, dtype: int, Q, K, Vt, O, tiles, soff, vlen, H: int, window_half: int, scale: float, qtile: int = 64,
+              gq=None, grow=None, stream=None):
+    """The engine's attention kernel on torch device tensors in the packed layout of laya_ext.h
+    (Q, K [rows, ldqk]; Vt [H*64, ldv]; O [.., ldo]; tiles int32 [n, 4]; soff, vlen int32)."""
+    import torch
+    st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    rc = lib.laya_ext_attention(dtype, Q.data_ptr(), K.data_ptr(), Q.shape[1], Q.shape[0], Vt.data_ptr(), Vt.shape[1],
+                                O.data_ptr(), O.shape[1], tiles.data_ptr(), tiles.shape[0], qtile, H, soff.data_ptr(),
+                                vlen.data_ptr(), ptr(gq), ptr(grow), window_half, scale, ctypes.c_void_p(st))
+    if rc != 0:
+        raise ValueError("attention arguments rejected")
+
+
 class Engine:
-    """One engine handle (not thread-safe; the engine lives until the process exits)."""
+    """One engine handle (not thread-safe; the engine lives until the process exits).
+
+    precision and env set LAYA_* variables (None: unset) for the duration of laya_create only: the
+    engine reads its configuration there, and the caller's environment is restored afterwards, so
+    one engine's settings never leak into the next."""
 
     def __init__(self, lib_path_: Optional[str], model_dir: str, precision: Optional[str] = None, env=None):
+        want = dict(env or {})
         if precision is not None:
-            os.environ["LAYA_PRECISION"] = precision
-        for k, v in (env or {}).items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = str(v)
+            want["LAYA_PRECISION"] = precision
+        saved = {k: os.environ.get(k) for k in want}
         self.lib = L = load_library(lib_path_)
-        self.h = L.laya_create(model_dir.encode())
+        try:
+            for k, v in want.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = str(v)
+            self.h = L.laya_create(model_dir.encode())
+        finally:
+            for k, v in saved.items():
+                if v is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = v
         if not self.h:
             raise RuntimeError("laya_create failed for %s" % model_dir)
         self.n_act = L.laya_n_act(self.h)
@@ -178,24 +215,15 @@ class Engine:
 
     # --- the reference server's call shape (server/laya_server.py:33-50)
     def forward_batch(self, seqs: List[List[int]], markers: List[List[int]], qtypes: List[int]):
-        B = len(seqs)
-        lens = array("i", (len(s) for s in seqs))
-        nm = array("i", (len(m) for m in markers))
-        ids = array("i", itertools.chain.from_iterable(seqs))
-        mk = array("i", itertools.chain.from_iterable(markers))
-        qt = array("i", qtypes)
-        buf = lambda a: (ctypes.c_int * len(a)).from_buffer(a) if len(a) else (ctypes.c_int * 1)()
-        lo = (ctypes.c_float * max(1, len(mk)))()
-        ac = (ctypes.c_float * max(1, B * self.n_act))()
-        if self.lib.laya_forward_batch(self.h, B, buf(lens), buf(ids), buf(nm), buf(mk), buf(qt), lo, ac) != 0:
-            raise ValueError("engine rejected batch (sequence too long or too many options)")
-        lo = np.ctypeslib.as_array(lo)[:len(mk)]
-        ac = np.ctypeslib.as_array(ac)[:B * self.n_act].reshape(B, self.n_act)
-        out, off = [], 0
-        for m in markers:
-            out.append(lo[off:off + len(m)].copy())
-            off += len(m)
-        return out, ac.copy()
+        """Questions as Python lists (token ids, marker positions, qtype each), all in one
+        laya_forward_batch call.  Returns one logits array per question and the [B, n_act] act
+        logits; raises ValueError when the engine rejects the batch."""
+        def cat(lists):
+            return np.fromiter((v for l in lists for v in l), np.int32) if lists else np.zeros(0, np.int32)
+        nmark = np.fromiter(map(len, markers), np.int32, len(markers))
+        logits, act = self.forward_flat(np.fromiter(map(len, seqs), np.int32, len(seqs)), cat(seqs), nmark,
+                                        cat(markers), np.asarray(qtypes, np.int32))
+        return np.split(logits, np.cumsum(nmark)[:-1]) if len(nmark) else [], act
 
     # --- flat numpy arrays, exactly the ABI's arguments
     def forward_flat(self, lens, ids, nmark, markers, qtypes):
@@ -212,7 +240,8 @@ class Engine:
                                          _ptr(qtypes, ctypes.c_int), _ptr(logits, ctypes.c_float),
                                          _ptr(act, ctypes.c_float))
         if rc != 0:
-            raise ValueError("engine rejected batch (sequence too long or too many options)")
+            raise ValueError("laya_forward_batch returned %d: a length, marker count, marker position, qtype or "
+                             "token id is outside the engine's limits" % rc)
         return logits[:int(nmark.sum())], act[:B * self.n_act].reshape(B, self.n_act)
 
     def forward_rc(self, lens, ids, nmark, markers, qtypes) -> int:
@@ -263,6 +292,13 @@ class Engine:
             out[name.value.decode()] = (ms.value, calls.value)
             i += 1
         return out
+
+    def stats(self):
+        """(graphs cached, graphs captured, tuned GEMM plans, tuned pass buckets)."""
+        out = (ctypes.c_longlong * 4)()
+        if self.lib.laya_ext_stats(self.h, out, 4) != 0:
+            raise RuntimeError("laya_ext_stats failed")
+        return tuple(int(x) for x in out)
 
     def replay(self, iters: int) -> float:
         ms = ctypes.c_float()

@@ -186,12 +186,3 @@ def run_per_question(W: Weights, cfg, batch, capture_rows=False):
     out = (np.concatenate(logits), np.stack(acts))
     return out + (caps,) if capture_rows else out
 
-
-def softmax_groups(flat_logits: np.ndarray, nmark) -> list:
-    out, o = [], 0
-    for k in nmark:
-        z = np.asarray(flat_logits[o:o + k], np.float64)
-        e = np.exp(z - z.max())
-        out.append(e / e.sum())
-        o += k
-    return out

@@ -14,8 +14,16 @@ Output (data only; no reference code is copied):
       input_ids/attention_mask/marker_pos/marker_mask/qtype, float32 logits/act_logits, and
       for the "dump" cases float32 [n, L, D] emb/enc*/final_norm/head* (right-padded rows).
   tests/golden/<large|base>/golden.npz             full-size configs: inputs, logits, act
-      logits, the bf16-autocast logits of the same model (its own drift), and per layer a few
-      sampled rows plus per-layer row statistics.
+      logits, the bf16-autocast logits of the same model (its own drift, as ref/bf16_drift.py
+      measures it), and per layer a few sampled rows plus per-layer row statistics, in fp32 and
+      under the same bf16 autocast (<layer>_rows_bf16_autocast: the reference's own per-layer
+      bf16 drift, the bar for the engine's bf16 path).  The autocast values depend on the host's
+      bf16 GEMM kernels: another thread count sums in another order, about one bf16 ulp of a logit.
+  tests/golden/<c3|c4|c5>_sample/drift.npz          a few questions of the bf16 benchmark batches
+      (ModernBERT-large b32 x s512, mmBERT-base b16 x s1024, ModernBERT-large-1024 b64 varlen) run
+      by the reference in fp32 and under bf16 autocast: fp32 and autocast logits and act logits,
+      and per layer the reference's own bf16 drift over all valid rows, max |x_bf16 - x_fp32| /
+      rms(x_fp32 row) (scalars only; the engine's fp32 side is the oracle on the GPU host).
 """
 import argparse
 import json
@@ -146,13 +154,16 @@ def full_size(out_root, work, preset, batch_fn, tag):
         a = acts[k][0, :int(b.lens[0])]
         rec[k + "_rows"] = a[rows].astype(np.float32)
         rec[k + "_stats"] = np.array([a.mean(), np.abs(a).max(), np.sqrt((a.astype(np.float64) ** 2).sum())], np.float64)
-    for h in hs:
-        h.remove()
+    acts.clear()
     with torch.no_grad(), torch.autocast("cpu", dtype=torch.bfloat16):
         l16, a16 = model(torch.as_tensor(ids), torch.as_tensor(att), torch.as_tensor(mpos),
                          torch.as_tensor(mmask), torch.as_tensor(qt))
+    for h in hs:
+        h.remove()
     rec["logits_bf16_autocast"] = l16.float().numpy()
     rec["act_logits_bf16_autocast"] = a16.float().numpy()
+    for k in names:
+        rec[k + "_rows_bf16_autocast"] = acts[k][0, :int(b.lens[0])][rows].astype(np.float32)
     os.makedirs(os.path.join(out_root, tag), exist_ok=True)
     np.savez(os.path.join(out_root, tag, "golden.npz"), **rec)
     with open(os.path.join(out_root, tag, "manifest.json"), "w") as f:
@@ -162,20 +173,62 @@ def full_size(out_root, work, preset, batch_fn, tag):
     print("[golden] %s: lens=%s logits=%s" % (tag, list(b.lens), logits.tolist()), flush=True)
 
 
+def batch_drift(out_root, work, preset, batch, tag):
+    """The reference's own bf16-autocast drift on a few questions of a benchmark batch."""
+    cfg = ck.PRESETS[preset]
+    mdir = ck.write_checkpoint(os.path.join(work, preset), cfg, seed=0)
+    model = load_reference_model(mdir)
+    acts, acts16 = {}, {}
+    hs = hooks(model, acts)
+    _, logits, act = run(model, batch, acts)
+    fp32 = {k: v.copy() for k, v in acts.items()}
+    ids, att, mpos, mmask, qt = batch.padded()
+    acts.clear()
+    with torch.no_grad(), torch.autocast("cpu", dtype=torch.bfloat16):
+        l16, a16 = model(torch.as_tensor(ids), torch.as_tensor(att), torch.as_tensor(mpos),
+                         torch.as_tensor(mmask), torch.as_tensor(qt))
+    for h in hs:
+        h.remove()
+    names = ["emb"] + ["enc%d" % i for i in range(cfg.n_layers)] + ["final_norm"] + \
+            ["head%d" % i for i in range(cfg.head_layers - 1)]
+    drift = np.zeros((len(names), batch.B))
+    for li, k in enumerate(names):
+        for i in range(batch.B):
+            a = fp32[k][i, :int(batch.lens[i])].astype(np.float64)
+            b = acts[k][i, :int(batch.lens[i])].astype(np.float64)
+            rms = np.sqrt((a ** 2).mean(1))
+            drift[li, i] = (np.abs(b - a).max(1) / rms).max()
+    rec = {"lens": np.asarray(batch.lens, np.int32), "nmark": batch.nmark, "layers": np.array(names),
+           "rel_drift_bf16_autocast": drift, "logits": logits, "act_logits": act,
+           "logits_bf16_autocast": l16.float().numpy(), "act_logits_bf16_autocast": a16.float().numpy()}
+    os.makedirs(os.path.join(out_root, tag), exist_ok=True)
+    np.savez(os.path.join(out_root, tag, "drift.npz"), **rec)
+    print("[golden] %s: lens=%s worst layer drift %.4f" % (tag, list(batch.lens), drift.max()), flush=True)
+
+
+# questions of the bf16 benchmark batches whose reference bf16 drift is recorded
+DRIFT_SAMPLES = {"c3_sample": ("large", "c3", [0, 1, 2, 3]), "c4_sample": ("base", "c4", [11, 15]),
+                 "c5_sample": ("large1024", "c5", [50, 17, 24])}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default="")
     ap.add_argument("--work", default=os.path.join(tempfile.gettempdir(), "laya_golden_ckpt"))
+    ap.add_argument("--out", default=HERE, help="output root (default: next to this script)")
     a = ap.parse_args()
     torch.set_grad_enabled(False)
     if a.only in ("", "tiny"):
-        tiny(HERE, a.work)
+        tiny(a.out, a.work)
     if a.only in ("", "large"):
-        full_size(HERE, a.work, "large", lambda: wl.c1(0), "large")
+        full_size(a.out, a.work, "large", lambda: wl.c1(0), "large")
     if a.only in ("", "base"):
         cfg = ck.PRESETS["base"]
-        full_size(HERE, a.work, "base", lambda: wl.make_batch(cfg, [200], [4], seed=7, dtype="fp32",
-                                                              name="base-b1s200"), "base")
+        full_size(a.out, a.work, "base", lambda: wl.make_batch(cfg, [200], [4], seed=7, dtype="fp32",
+                                                               name="base-b1s200"), "base")
+    for tag, (preset, wname, pick) in DRIFT_SAMPLES.items():
+        if a.only in ("", tag):
+            batch_drift(a.out, a.work, preset, wl.CONFIGS[wname](0).subset(pick), tag)
 
 
 if __name__ == "__main__":

@@ -48,3 +48,14 @@ def test_binding_covers_the_headers():
 def test_product_library_does_not_link_the_oracle():
     data = open(le.DEFAULT_LIB, "rb").read()
     assert b"oracle" not in data and b"torch" not in data
+
+
+@pytest.mark.parametrize("tool", ["laya-parity", "laya-bench"])
+def test_cpp_tools_are_built_and_start_without_a_gpu(lib, tool):
+    """The C++ callers of laya_api.h (built next to liblaya.so) link it and print their usage
+    without touching a GPU when given no arguments."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(le.DEFAULT_LIB), tool)
+    assert os.path.exists(exe)
+    r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stdout

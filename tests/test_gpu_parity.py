@@ -5,8 +5,14 @@ Bars (from the engine's acceptance criteria):
   fp32 path: hidden states after every layer within max-abs 1e-3 of the reference fp32 PyTorch
              model; output probabilities within 1e-4; act logits within 1e-3 (relative to
              max(1, |x|)).
-  bf16 path: drift budget stated per test (bf16 weights and GEMM operands, fp32 residual,
-             softmax and logits) -- see BF16_* below.
+  bf16 path (bf16 weights and GEMM/attention operands; fp32 residual, LayerNorm, softmax, logits
+             and act head): the reference's own bf16 path (its model under bf16 autocast, as
+             ref/bf16_drift.py runs it) recorded on the same inputs is the bar.  Per layer, the
+             engine's drift from the fp32 reference, max |x - x_ref| / rms(x_ref row), stays within
+             BF16_VS_UPSTREAM times the reference's bf16 drift plus BF16_FLOOR_REL; logits and act
+             logits within BF16_VS_UPSTREAM times the reference's bf16 deviation plus
+             BF16_FLOOR_LOGIT.  Where no reference bf16 run exists (the tiny model), hidden states
+             stay within BF16_HIDDEN_REL of the layer RMS.
 Integer/index work (packing, gathering, graph replay) is checked bit-exactly.
 """
 import json
@@ -26,12 +32,26 @@ pytestmark = pytest.mark.gpu
 FP32_HIDDEN = 1e-3
 FP32_PROB = 1e-4
 FP32_ACT = 1e-3
-# bf16 drift budget: probabilities of every question within 0.02 of the fp32 reference, hidden
-# states within 5e-2 relative to the layer's RMS
-BF16_PROB = 2e-2
-BF16_HIDDEN_REL = 5e-2
+# bf16 drift budgets (see the module docstring).  Measured on MI355X: past the first layers the
+# engine's per-layer drift is 0.6-1.2x the reference's bf16 drift, and its logit and act deviations
+# 0.2-1.2x the reference's (ModernBERT-large b1 x s128, samples of the b32 x s512, b16 x s1024 and
+# b64 varlen batches).  The floor is one bf16 rounding of the embedding rows, which the engine
+# stores in bf16 and the reference keeps in fp32: 0.012-0.013 of the row RMS at the embedding
+# output, where the reference's bf16 drift is 0.
+BF16_VS_UPSTREAM = 2.0
+BF16_FLOOR_REL = 2.0 ** -6
+BF16_FLOOR_LOGIT = 1e-3
+# the tiny model (no reference bf16 run): measured at most 0.0114 of the row RMS per layer, 3e-4 in
+# logits and act logits, 5e-5 in probabilities
+BF16_HIDDEN_REL = 2.5e-2
+BF16_TINY_LOGIT = 2e-3
+BF16_PROB = 1e-3
 
-ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1}
+# every knob laya_create reads, pinned to its default unless a test sets it (Engine() applies them
+# for laya_create only, so nothing leaks from one engine to the next)
+ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
+       "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None}
 _ENGINES = {}
 
 
@@ -257,20 +277,25 @@ def test_tiny_layer_by_layer(precision):
                     if precision == "fp32":
                         assert err < FP32_HIDDEN, (case["name"], name, i, err)
                     else:
-                        rms = np.sqrt((ref ** 2).mean())
-                        assert err / rms < BF16_HIDDEN_REL * 4, (case["name"], name, i, err, rms)
-            # last head layer: gathered rows = every marker row in question order, then CLS rows
+                        rel = float((np.abs(g - ref).max(1) / np.sqrt((ref ** 2).mean(1))).max())
+                        print("tiny bf16 %s %-6s q%d rel drift %.4f" % (case["name"], name, i, rel))
+                        assert rel < BF16_HIDDEN_REL, (case["name"], name, i, rel)
+            # last head layer: gathered rows = every marker row in question order, padded to a
+            # multiple of 64 rows, then CLS rows
             got = _dump_rows(dd, "head1_gathered", cfg.d)
-            KT = int(nm.sum())
+            KT = (int(nm.sum()) + 63) // 64 * 64
             o = 0
             for i in range(len(lens)):
-                for kk in range(nm[i]):
-                    ref = c["head1"][i, mk[o + kk]]
-                    err = np.abs(got[o + kk] - ref).max()
-                    assert err < (FP32_HIDDEN if precision == "fp32" else 0.2), (case["name"], "head1", err)
+                rows = [o + kk for kk in range(nm[i])] + [KT + i]
+                ref = c["head1"][i, list(mk[o:o + nm[i]]) + [0]].astype(np.float64)
+                if precision == "fp32":
+                    err = np.abs(got[rows] - ref).max()
+                    assert err < FP32_HIDDEN, (case["name"], "head1", i, err)
+                else:
+                    rel = float((np.abs(got[rows] - ref).max(1) / np.sqrt((ref ** 2).mean(1))).max())
+                    print("tiny bf16 %s head1  q%d rel drift %.4f" % (case["name"], i, rel))
+                    assert rel < BF16_HIDDEN_REL, (case["name"], "head1", i, rel)
                 o += nm[i]
-                err = np.abs(got[KT + i] - c["head1"][i, 0]).max()
-                assert err < (FP32_HIDDEN if precision == "fp32" else 0.2), (case["name"], "head1 cls", err)
 
 
 @pytest.mark.parametrize("case", [c["name"] for c in tiny_cases()])
@@ -278,9 +303,12 @@ def test_tiny_bf16_drift(case):
     c = read_tiny_case(next(x for x in tiny_cases() if x["name"] == case))
     args = unpad_case(c)
     logits, act = engine("tiny", "bf16").forward_flat(*args)
-    d = prob_delta(logits, golden_flat_logits(c), args[2])
-    print("bf16 drift %s: dprob %.5f" % (case, d))
-    assert d < BF16_PROB
+    gl = golden_flat_logits(c)
+    d = prob_delta(logits, gl, args[2])
+    dl = float(np.abs(logits - gl).max())
+    da = float(np.abs(act - c["act_logits"]).max())
+    print("bf16 drift %s: dprob %.5f dlogit %.5f dact %.5f" % (case, d, dl, da))
+    assert d < BF16_PROB and dl < BF16_TINY_LOGIT and da < BF16_TINY_LOGIT
 
 
 # ---------------------------------------------------------------- packing / graphs / validation
@@ -322,7 +350,9 @@ def test_tiny_extremes_vs_oracle(precision):
     if precision == "fp32":
         assert np.abs(lo - ref_lo).max() < 1e-4 and d < FP32_PROB and da < FP32_ACT, (d, da)
     else:
-        assert d < BF16_PROB, d
+        dl, dA = float(np.abs(lo - ref_lo).max()), float(np.abs(ac - ref_ac).max())
+        print("tiny extremes bf16: dprob %.5f dlogit %.5f dact %.5f" % (d, dl, dA))
+        assert d < BF16_PROB and dl < BF16_TINY_LOGIT and dA < BF16_TINY_LOGIT, (d, dl, dA)
 
 
 def test_graph_replay_matches_eager():
@@ -419,18 +449,49 @@ def test_base_fp32_golden():
     _full_size_fp32_golden("base", b)
 
 
-def test_large_bf16_c1_drift():
-    """bf16 path on the same input: drift against the fp32 reference, next to the reference's own
-    bf16-autocast drift on that input (both recorded in the golden file)."""
+def _rel_drift(got, ref):
+    """max over rows of max |got - ref| / rms(ref row)."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float((np.abs(got - ref).max(-1) / np.sqrt((ref ** 2).mean(-1))).max())
+
+
+def test_large_bf16_c1_layer_drift():
+    """bf16 engine, ModernBERT-large + head at b1 x s128: per layer, the sampled rows' drift from the
+    reference's fp32 rows against the reference's own bf16-autocast drift on the same rows; then
+    logits and act logits against the reference's bf16 deviation."""
     g = np.load(os.path.join(GOLDEN, "large", "golden.npz"))
+    man = json.load(open(os.path.join(GOLDEN, "large", "manifest.json")))
     b = wl.c1(0)
     lens, ids, nm, mk, qt = b.flat()
-    lo, ac = engine("large", "bf16").forward_flat(lens, ids, nm, mk, qt)
-    gl = g["logits"][0, :nm[0]]
-    ours = prob_delta(lo, gl, nm)
-    upstream = prob_delta(g["logits_bf16_autocast"][0, :nm[0]], gl, nm)
-    print("large bf16 dprob: engine %.5f, reference bf16 autocast %.5f" % (ours, upstream))
-    assert ours < BF16_PROB
+    W_type = ck.read_safetensors(os.path.join(checkpoint_dir("large"), "model.safetensors"))["type_emb.weight"]
+    rows = g["sample_rows"]
+    with tempfile.TemporaryDirectory() as dd:
+        lo, ac = engine("large", "bf16", LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0).forward_flat(lens, ids, nm, mk, qt)
+        worst = 0.0
+        for name in man["layers"]:
+            ref, ref16 = g[name + "_rows"].astype(np.float64), g[name + "_rows_bf16_autocast"].astype(np.float64)
+            if name == "head1":
+                # the last head layer runs on the gathered rows only: CLS (row 0) and the markers
+                keep = [j for j, r in enumerate(rows) if r == 0 or r in set(mk)]
+                KT = (int(nm.sum()) + 63) // 64 * 64
+                gath = _dump_rows(dd, "head1_gathered", 1024)
+                got = np.stack([gath[KT] if rows[j] == 0 else gath[list(mk).index(rows[j])] for j in keep])
+                ref, ref16 = ref[keep], ref16[keep]
+            else:
+                got = _dump_rows(dd, {"final_norm": "final"}.get(name, name), 1024)[rows].astype(np.float64)
+                if name == "final_norm":          # the engine's final rows carry the type embedding
+                    got = got - W_type[qt[0]]
+            eng, up = _rel_drift(got, ref), _rel_drift(ref16, ref)
+            worst = max(worst, eng / (up + BF16_FLOOR_REL))
+            print("large c1 bf16 %-10s engine %.4f reference-bf16 %.4f" % (name, eng, up))
+            assert eng <= BF16_VS_UPSTREAM * up + BF16_FLOOR_REL, (name, eng, up)
+    gl, g16 = g["logits"][0, :nm[0]], g["logits_bf16_autocast"][0, :nm[0]]
+    dl, dl_up = float(np.abs(lo - gl).max()), float(np.abs(g16 - gl).max())
+    da, da_up = float(np.abs(ac - g["act_logits"]).max()), float(np.abs(g["act_logits_bf16_autocast"] - g["act_logits"]).max())
+    print("large c1 bf16 dlogit engine %.5f reference-bf16 %.5f; dact engine %.5f reference-bf16 %.5f; "
+          "dprob engine %.5f reference-bf16 %.5f" % (dl, dl_up, da, da_up, prob_delta(lo, gl, nm), prob_delta(g16, gl, nm)))
+    assert dl <= BF16_VS_UPSTREAM * dl_up + BF16_FLOOR_LOGIT
+    assert da <= BF16_VS_UPSTREAM * da_up + BF16_FLOOR_LOGIT
 
 
 def test_tile_configs_bit_identical():
@@ -482,67 +543,79 @@ def test_gemm_tuning_keeps_outputs():
     (LAYA_TUNE=0) agree exactly, before and after tune_all."""
     import time
     b = wl.c3(0).subset(list(range(8)))
-    lo0, ac0 = engine("large", "bf16", LAYA_TUNE=0).forward_flat(*b.flat())
-    e = engine("large", "bf16", LAYA_MAX_TOKENS=8192)
+    e0 = engine("large", "bf16", LAYA_TUNE=0)
+    lo0, ac0 = e0.forward_flat(*b.flat())
+    assert e0.stats()[2] == 0                           # the analytic planner only: nothing timed
+    e = le.Engine(None, checkpoint_dir("large"), precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=8192))
     lo1, ac1 = e.forward_flat(*b.flat())
+    tuned_pass = e.stats()[2]
+    assert tuned_pass > 0                               # the pass's GEMMs were timed before it ran
     t0 = time.time()
     e.tune_all()
-    print("tune_all over 8192 rows: %.2f s" % (time.time() - t0))
+    dt = time.time() - t0
+    st = e.stats()
+    print("tune_all over 8192 rows: %.2f s, %d plans over %d pass buckets" % (dt, st[2], st[3]))
+    assert st[2] > tuned_pass and st[3] >= 40           # every row bucket up to 8192 (40 buckets) was listed
     lo2, ac2 = e.forward_flat(*b.flat())
     assert np.isfinite(lo0).all() and np.isfinite(ac0).all()
     for lo, ac in ((lo1, ac1), (lo2, ac2)):
         assert np.array_equal(lo, lo0) and np.array_equal(ac, ac0)
 
 
-def test_base_bf16_c4_sample_vs_oracle():
-    """Two questions of the mmBERT-base-shaped b16 x s1024 batch (lengths 972 and 966) in bf16
-    against the fp32 CPU oracle."""
+# questions of the bf16 benchmark batches with the reference's bf16 drift recorded
+# (tests/golden/<tag>/drift.npz, written by make_golden.py): (checkpoint preset, batch, questions)
+SAMPLES = {"c3_sample": ("large", wl.c3, [0, 1, 2, 3]), "c4_sample": ("base", wl.c4, [11, 15]),
+           "c5_sample": ("large1024", wl.c5, [50, 17, 24])}
+
+
+@pytest.mark.parametrize("tag", list(SAMPLES))
+def test_bf16_sample_layer_drift(tag):
+    """bf16 engine on questions of the b32 x s512 (ModernBERT-large), b16 x s1024 (mmBERT-base) and
+    b64 varlen (ModernBERT-large-1024, 25-29 markers per sequence) batches: every valid row of every
+    layer against the fp32 CPU oracle, within BF16_VS_UPSTREAM times the reference's own bf16 drift
+    on the same questions; logits and act logits likewise.  For the varlen batch the whole
+    64-sequence pass (18k tokens) must give the same bits for these questions."""
     import torch
     from oracle import model as om
     torch.set_num_threads(min(16, os.cpu_count() or 1))
-    cfg, W = ck.load_checkpoint(checkpoint_dir("base"))
-    b = wl.c4(0).subset([11, 15])
-    lo, ac = engine("base", "bf16").forward_flat(*b.flat())
-    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["base"], b)
-    d = prob_delta(lo, ref_lo, b.nmark)
-    print("c4 sample bf16 dprob %.5f lens %s" % (d, list(b.lens)))
-    assert d < BF16_PROB
-
-
-def test_large1024_bf16_c5_sample_vs_oracle():
-    """Three sequences of the ModernBERT-large (1024 context) b64 x s1024 batch with 25-29 markers
-    each (eight questions of 2-5 options per sequence) in bf16 against the fp32 CPU oracle; the
-    whole 64-sequence batch (18k tokens, one pass) must give the same logits for them."""
-    import torch
-    from oracle import model as om
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
-    d = ck.cached_checkpoint("large1024")
-    cfg, W = ck.load_checkpoint(d)
-    full = wl.c5(0)
-    pick = [50, 17, 24]
+    preset, make, pick = SAMPLES[tag]
+    ref = np.load(os.path.join(GOLDEN, tag, "drift.npz"))
+    full = make(0)
     b = full.subset(pick)
-    e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=32768))
-    lo, ac = e.forward_flat(*b.flat())
-    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["large1024"], b)
-    dp = prob_delta(lo, ref_lo, b.nmark)
-    print("c5 sample bf16 dprob %.5f lens %s nmark %s" % (dp, list(b.lens), list(b.nmark)))
-    assert dp < BF16_PROB
-    flo, fac = e.forward_flat(*full.flat())
-    moff = np.concatenate([[0], np.cumsum(full.nmark)])
-    got = np.concatenate([flo[moff[i]:moff[i + 1]] for i in pick])
-    assert np.array_equal(got, lo)
-    assert np.array_equal(fac.reshape(64, -1)[pick], ac.reshape(len(pick), -1))
-
-
-def test_large_bf16_c3_sample_vs_oracle():
-    """Four questions of the bf16 b32 x s512 benchmark batch against the fp32 CPU oracle."""
-    import torch
-    from oracle import model as om
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
-    cfg, W = ck.load_checkpoint(checkpoint_dir("large"))
-    b = wl.c3(0).subset([0, 1, 2, 3])
-    lo, ac = engine("large", "bf16").forward_flat(*b.flat())
-    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["large"], b)
-    d = prob_delta(lo, ref_lo, b.nmark)
-    print("c3 sample bf16 dprob %.5f lens %s" % (d, list(b.lens)))
-    assert d < BF16_PROB
+    assert list(ref["lens"]) == list(b.lens)
+    d = ck.cached_checkpoint(preset)
+    cfg, W = ck.load_checkpoint(d)
+    ref_lo, ref_ac, caps = om.run_per_question(om.Weights(W), ck.PRESETS[preset], b, capture_rows=True)
+    lens, ids, nm, mk, qt = b.flat()
+    soff = np.concatenate([[0], np.cumsum((lens + 7) // 8 * 8)])
+    worst = (0.0, "")
+    with tempfile.TemporaryDirectory() as dd:
+        e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0))
+        lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
+        for li, name in enumerate(ref["layers"]):
+            got = _dump_rows(dd, {"final_norm": "final"}.get(str(name), str(name)), cfg.d)
+            for i in range(b.B):
+                r = caps[i][str(name)]
+                gi = got[soff[i]:soff[i] + lens[i]].astype(np.float64)
+                if name == "final_norm":
+                    gi = gi - W["type_emb.weight"][qt[i]]
+                eng, up = _rel_drift(gi, r), float(ref["rel_drift_bf16_autocast"][li, i])
+                worst = max(worst, (eng / (BF16_VS_UPSTREAM * up + BF16_FLOOR_REL), "%s q%d" % (name, i)))
+                if i == 0 or eng > BF16_VS_UPSTREAM * up + BF16_FLOOR_REL:
+                    print("%s bf16 %-10s q%d engine %.4f reference-bf16 %.4f" % (tag, name, i, eng, up))
+                assert eng <= BF16_VS_UPSTREAM * up + BF16_FLOOR_REL, (name, i, eng, up)
+    print("%s bf16 worst layer drift / budget %.3f (%s)" % (tag, worst[0], worst[1]))
+    up_lo = np.concatenate([ref["logits_bf16_autocast"][i, :nm[i]] - ref["logits"][i, :nm[i]] for i in range(b.B)])
+    dl, dl_up = float(np.abs(lo - ref_lo).max()), float(np.abs(up_lo).max())
+    da, da_up = float(np.abs(ac - ref_ac).max()), float(np.abs(ref["act_logits_bf16_autocast"] - ref["act_logits"]).max())
+    print("%s bf16 dlogit engine %.5f reference-bf16 %.5f; dact engine %.5f reference-bf16 %.5f; dprob %.5f"
+          % (tag, dl, dl_up, da, da_up, prob_delta(lo, ref_lo, nm)))
+    assert dl <= BF16_VS_UPSTREAM * dl_up + BF16_FLOOR_LOGIT
+    assert da <= BF16_VS_UPSTREAM * da_up + BF16_FLOOR_LOGIT
+    if tag == "c5_sample":
+        e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=32768))
+        flo, fac = e.forward_flat(*full.flat())
+        moff = np.concatenate([[0], np.cumsum(full.nmark)])
+        got = np.concatenate([flo[moff[i]:moff[i + 1]] for i in pick])
+        assert np.array_equal(got, e.forward_flat(lens, ids, nm, mk, qt)[0]) and np.array_equal(got, lo)
+        assert np.array_equal(fac.reshape(64, -1)[pick], ac.reshape(len(pick), -1))

@@ -1,0 +1,206 @@
+"""The engine as the reference's callers use it, on the GPU, through the C ABI:
+
+  * the reference server's warm-up (server/laya_server.py:52-56: laya_tune_all, then one call per
+    length 64, 128, ..., max_len) followed by mixed single-question and batched traffic: warmed
+    shapes replay their graphs without capturing, every answer equals the eager engine's bit for
+    bit, and a cache miss's cost (eager run + capture + instantiate) is measured;
+  * the graph cache limit (512 graphs, src/engine.hip:477): calls beyond it run eagerly and stay
+    correct;
+  * laya_tune_all at the default capacity (65536 rows), timed;
+  * checkpoints stored as F16, BF16 and F32 (src/engine.hip:115-129): a BF16 file gives exactly the
+    results of an F32 file holding the same values, in both engines; an F16 file on the fp32 engine
+    matches the CPU oracle run on the F16-rounded weights within the fp32 bars;
+  * the C++ tools (laya-parity on the reference golden format, laya-bench's latency table), which
+    call the library as any C caller of laya_api.h would.
+"""
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, checkpoint_dir
+from layamd_amd import checkpoint as ck
+from layamd_amd import engine as le
+from layamd_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
+       "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None}
+
+
+def make_engine(model_dir, precision, **env):
+    return le.Engine(None, model_dir, precision=precision, env=dict(ENV, **env))
+
+
+def same(a, b):
+    return np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_reference_warmup_then_traffic():
+    """ModernBERT-large bf16: the server's warm-up, then 24 single questions of random lengths
+    (<= 64 options: the warmed marker bucket) that must all replay warmed graphs, then batched
+    requests; every answer equals the eager (graph-free) engine's."""
+    cfg = ck.PRESETS["large"]
+    d = checkpoint_dir("large")
+    e = make_engine(d, "bf16")
+    eager = make_engine(d, "bf16", LAYA_GRAPHS=0)
+    t0 = time.time()
+    e.tune_all()
+    t_tune = time.time() - t0
+    t0 = time.time()
+    for n in range(64, cfg.max_len + 1, 64):                # server/laya_server.py:52-56
+        e.forward_batch([[cfg.cls_id] * n], [[1, 2]], [0])
+    t_warm = time.time() - t0
+    g0, c0, _, _ = e.stats()
+    print("warm-up: tune_all %.2f s, %d lengths %.2f s, %d graphs" % (t_tune, cfg.max_len // 64, t_warm, g0))
+    assert g0 == cfg.max_len // 64
+    rs = np.random.RandomState(7)
+    lat = []
+    for i in range(24):
+        L = int(rs.randint(1, cfg.max_len + 1))
+        k = int(rs.randint(1, 65))
+        b = wl.make_batch(cfg, [L], [k], seed=100 + i)
+        t = time.perf_counter()
+        r = e.forward_flat(*b.flat())
+        lat.append(1e3 * (time.perf_counter() - t))
+        assert same(r, eager.forward_flat(*b.flat())), (L, k)
+    assert e.stats()[1] == c0, "a warmed single-question shape captured a new graph"
+    print("single questions after warm-up: p50 %.2f ms, max %.2f ms over %d calls" % (np.median(lat), max(lat), len(lat)))
+    # batched traffic: new buckets (rows, questions, marker rows) are run eagerly, then captured
+    miss, hit = [], []
+    for i in range(6):
+        B = int(rs.randint(2, 9))
+        lens = rs.randint(16, cfg.max_len + 1, B)
+        b = wl.make_batch(cfg, lens, rs.randint(2, 6, B), seed=200 + i)
+        n_before = e.stats()[1]
+        t = time.perf_counter()
+        r1 = e.forward_flat(*b.flat())
+        t1 = 1e3 * (time.perf_counter() - t)
+        t = time.perf_counter()
+        r2 = e.forward_flat(*b.flat())
+        t2 = 1e3 * (time.perf_counter() - t)
+        assert same(r1, r2) and same(r1, eager.forward_flat(*b.flat()))
+        if e.stats()[1] > n_before:
+            miss.append(t1)
+            hit.append(t2)
+    print("batched requests: first call of a new bucket (eager + capture) %s ms, replay %s ms"
+          % (np.round(miss, 2).tolist(), np.round(hit, 2).tolist()))
+
+
+def test_graph_cache_limit():
+    """At most LAYA_MAX_GRAPHS graphs (default 512, the reference's limit) are kept; the 513th and
+    later buckets run eagerly, give the eager engine's bits, and evict nothing."""
+    cfg = ck.PRESETS["tiny"]
+    d = checkpoint_dir("tiny")
+    e = make_engine(d, "bf16", LAYA_MAX_TOKENS=4096)
+    eager = make_engine(d, "bf16", LAYA_MAX_TOKENS=4096, LAYA_GRAPHS=0)
+    first = None
+    t0 = time.time()
+    # 520 buckets (rows, questions, marker rows): 1..260 one-token questions with one option each
+    # (64 marker rows) and with 64 options each (64 B marker rows)
+    for n, (B, k) in enumerate([(B, 1) for B in range(1, 261)] + [(B, 64) for B in range(1, 261)]):
+        b = wl.make_batch(cfg, [1] * B, [k] * B, seed=n)
+        r = e.forward_flat(*b.flat())
+        if n == 0:
+            first = (b, r)
+        if n in (0, 259, 510, 511, 512, 513, 519):
+            assert same(r, eager.forward_flat(*b.flat())), n
+    g, c, _, _ = e.stats()
+    print("520 buckets in %.1f s: %d graphs cached, %d captured" % (time.time() - t0, g, c))
+    assert g == 512 and c == 512
+    assert same(e.forward_flat(*first[0].flat()), first[1])     # still replays the first graph
+    small = make_engine(d, "fp32", LAYA_MAX_GRAPHS=2)
+    for B in (1, 2, 3, 4):
+        b = wl.make_batch(cfg, [40] * B, [2] * B, seed=B)
+        assert same(small.forward_flat(*b.flat()), small.forward_flat(*b.flat()))
+    assert small.stats()[:2] == (2, 2)
+
+
+def test_tune_all_default_capacity():
+    """laya_tune_all at the default capacity (65536 rows: 88 row buckets of every GEMM), timed;
+    the tuned engine gives the untuned engine's bits."""
+    d = checkpoint_dir("large")
+    e = make_engine(d, "bf16", LAYA_MAX_TOKENS=None)
+    t0 = time.time()
+    e.tune_all()
+    dt = time.time() - t0
+    g, c, plans, buckets = e.stats()
+    print("tune_all at 65536 rows: %.1f s, %d GEMM plans over %d row buckets" % (dt, plans, buckets))
+    assert buckets >= 88
+    b = wl.c3(0).subset(list(range(6)))
+    assert same(e.forward_flat(*b.flat()), make_engine(d, "bf16", LAYA_TUNE=0).forward_flat(*b.flat()))
+
+
+def _f32_copy(preset, dtype, **kw):
+    """(dir of the dtype file, dir of an F32 file holding exactly its values)."""
+    return ck.cached_checkpoint(preset, dtype=dtype, **kw), ck.cached_checkpoint(preset, dtype="F32", round_to=dtype, **kw)
+
+
+@pytest.mark.parametrize("dtype", ["BF16", "F16"])
+def test_checkpoint_dtypes_tiny(dtype):
+    """Tiny model (LayerNorm weights and biases perturbed so every parameter matters): an F16 or BF16
+    file equals the F32 file of the same values in both engines, bit for bit; the fp32 engine on it
+    matches the oracle on the rounded weights."""
+    from oracle import model as om
+    dfile, df32 = _f32_copy("tiny", dtype, ln_jitter=0.1)
+    b = wl.make_batch(ck.PRESETS["tiny"], [5, 64, 129, 320, 1], [2, 3, 12, 4, 1], seed=9)
+    for prec in ("fp32", "bf16"):
+        assert same(make_engine(dfile, prec).forward_flat(*b.flat()), make_engine(df32, prec).forward_flat(*b.flat())), prec
+    cfg, W = ck.load_checkpoint(dfile)
+    lo, ac = make_engine(dfile, "fp32").forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["tiny"], b)
+    assert np.abs(lo - ref_lo).max() < 1e-4
+    assert (np.abs(ac - ref_ac) / np.maximum(1.0, np.abs(ref_ac))).max() < 1e-3
+
+
+def test_checkpoint_dtypes_large():
+    """ModernBERT-large at b1 x s128: the BF16 file equals the F32 file of its values in the bf16
+    engine bit for bit; the fp32 engine on the F16 file matches the oracle on the F16 weights
+    (probabilities within 1e-4, act logits within 1e-3)."""
+    import torch
+    from oracle import model as om
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    b = wl.c1(0)
+    dfile, df32 = _f32_copy("large", "BF16")
+    assert same(make_engine(dfile, "bf16").forward_flat(*b.flat()), make_engine(df32, "bf16").forward_flat(*b.flat()))
+    d16 = ck.cached_checkpoint("large", dtype="F16")
+    cfg, W = ck.load_checkpoint(d16)
+    lo, ac = make_engine(d16, "fp32").forward_flat(*b.flat())
+    ref_lo, ref_ac = om.run_batch(om.Weights(W), ck.PRESETS["large"], b)
+    p = lambda z: np.exp(z - z.max()) / np.exp(z - z.max()).sum()
+    assert np.abs(p(lo) - p(ref_lo)).max() < 1e-4
+    assert (np.abs(ac - ref_ac) / np.maximum(1.0, np.abs(ref_ac))).max() < 1e-3
+
+
+def _tool(name):
+    exe = os.path.join(os.path.dirname(le.DEFAULT_LIB), name)
+    assert os.path.exists(exe), "%s not built (python -m layamd_amd.build)" % exe
+    return exe
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_cpp_parity_tool_on_golden_format(precision):
+    """laya-parity, a C++ program calling only laya_api.h, reads the reference golden format
+    (tests/golden/tiny) and passes: fp32 at the fp32 bars, bf16 at the reference tool's bars."""
+    env = dict(os.environ, LAYA_PRECISION=precision, LAYA_MAX_TOKENS="4096")
+    tol = ["--prob-tol", "1e-4", "--act-tol", "1e-3", "--logit-tol", "1e-4"] if precision == "fp32" else []
+    r = subprocess.run([_tool("laya-parity"), checkpoint_dir("tiny"), os.path.join(GOLDEN, "tiny")] + tol, env=env,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=300)
+    print(r.stdout[-3000:])
+    assert r.returncode == 0
+    assert "questions pass" in r.stdout
+
+
+def test_cpp_latency_tool():
+    """laya-bench, the ABI latency table (p50 per laya_forward_batch call, host work included) on
+    ModernBERT-large bf16."""
+    env = dict(os.environ, LAYA_PRECISION="bf16", LAYA_MAX_TOKENS="16384")
+    r = subprocess.run([_tool("laya-bench"), checkpoint_dir("large"), "--iters", "20"], env=env,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
+    print(r.stdout[-4000:])
+    assert r.returncode == 0 and "batched" in r.stdout

@@ -45,14 +45,14 @@ def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=5
     if n < 0:
         return None
     out = []
-    T = int(np.sum((np.asarray(lens) + 7) // 8 * 8)) + 1
-    R = int(np.sum(nm)) + len(lens) + 1
+    T = int(np.sum((np.asarray(lens) + 7) // 8 * 8)) + 64
+    R = int(np.sum(nm)) + len(lens) + 64
     for w in range(n):
         dims = np.zeros(10, np.int32)
         rows = np.zeros(3 * T, np.int32)
         seqs = np.zeros(5 * len(lens) + 1, np.int32)
-        tiles = np.zeros(4 * (T // 64 + len(lens) + 1), np.int32)
-        gtiles = np.zeros(4 * (R // 64 + len(lens) + 1), np.int32)
+        tiles = np.zeros(4 * (T // 64 + len(lens)), np.int32)
+        gtiles = np.zeros(4 * (R // 64 + len(lens)), np.int32)
         gq = np.zeros(R, np.int32)
         grow = np.zeros(R, np.int32)
         bufs = [P(x)[1] for x in (dims, rows, seqs, tiles, gtiles, gq, grow)]
@@ -83,15 +83,22 @@ def test_validation_minus_one(host):
     assert plan(host, [], [], [], [], []) == []                            # empty call: no pass
 
 
+def up64(x):
+    return (int(x) + 63) // 64 * 64
+
+
 @pytest.mark.parametrize("q_tile", [64, 128])
 def test_layout_of_a_pass(host, q_tile):
     cfg = ck.PRESETS["tiny"]
     b = wl.make_batch(cfg, [1, 64, 65, 200, 17, 128, 129, 256], [1, 3, 255, 12, 2, 1, 4, 2], seed=1)
     (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, q_tile=q_tile)
     rows8 = (b.lens + 7) // 8 * 8                                          # questions start on 8-row groups
-    assert p["B"] == b.B and p["T"] == int(rows8.sum()) and p["valid"] == int(b.lens.sum())
+    # the pass's rows are padded to a multiple of 64 (its graph bucket)
+    assert p["B"] == b.B and p["T"] == up64(rows8.sum()) and p["valid"] == int(b.lens.sum())
     soff = np.concatenate([[0], np.cumsum(rows8)])
     assert np.array_equal(p["soff"], soff)
+    tail = slice(soff[-1], p["T"])                                         # bucket padding rows
+    assert np.all(p["ids"][tail] == cfg.pad_id) and np.all(p["pos"][tail] == 0) and np.all(p["seq"][tail] == b.B - 1)
     for i in range(b.B):
         r = slice(soff[i], soff[i + 1])
         assert np.array_equal(p["ids"][r][:b.lens[i]], b.ids[i])
@@ -100,30 +107,40 @@ def test_layout_of_a_pass(host, q_tile):
         assert np.all(p["seq"][r] == i)
         assert soff[i] % 8 == 0
     # encoder tiles: every valid row of every question exactly once, <= q_tile queries, inside its
-    # question, a full tile unless it holds the question's last row
+    # question, a full tile unless it holds the question's last row; the list is padded with empty
+    # tiles to the bucket's capacity T / 64 + B
+    assert len(p["tiles"]) == p["T"] // 64 + b.B
+    real = p["tiles"][p["tiles"][:, 2] > 0]
+    assert np.all(p["tiles"][len(real):] == 0)
     cover = np.zeros(p["T"], int)
-    for seq, q0, nq, _ in p["tiles"]:
+    for seq, q0, nq, _ in real:
         assert 1 <= nq <= q_tile and q0 % q_tile == 0 and q0 + nq <= b.lens[seq]
         assert nq == q_tile or q0 + nq == b.lens[seq]
         cover[soff[seq] + q0: soff[seq] + q0 + nq] += 1
     valid_rows = np.concatenate([np.arange(soff[i], soff[i] + b.lens[i]) for i in range(b.B)])
     assert np.all(cover[valid_rows] == 1) and cover.sum() == p["valid"]
-    # gathered rows: markers in question order, then one CLS row per question
-    KT = int(b.nmark.sum())
+    # gathered rows: markers in question order, padded with row 0 to a multiple of 64, then one CLS
+    # row per question
+    nmk = int(b.nmark.sum())
+    KT = up64(nmk)
     assert p["KT"] == KT and p["R"] == KT + b.B
     mk = np.concatenate(b.markers)
     moff = np.concatenate([[0], np.cumsum(b.nmark)])
     assert np.array_equal(p["moff"], moff[:-1])
+    assert np.all(p["grow"][nmk:KT] == 0)
     for i in range(b.B):
         assert np.array_equal(p["grow"][moff[i]:moff[i + 1]], soff[i] + mk[moff[i]:moff[i + 1]])
         assert p["grow"][KT + i] == soff[i]
+    assert len(p["gtiles"]) == p["R"] // 64 + b.B
+    greal = p["gtiles"][p["gtiles"][:, 2] > 0]
+    assert np.all(p["gtiles"][len(greal):] == 0)
     seen = np.zeros(p["R"], int)
-    for seq, start, nq, _ in p["gtiles"]:
+    for seq, start, nq, _ in greal:
         assert 1 <= nq <= 64
         for gi in p["gq"][start:start + nq]:
             seen[gi] += 1
             assert soff[seq] <= p["grow"][gi] < soff[seq] + b.lens[seq]
-    assert np.all(seen == 1)
+    assert np.all(seen[:nmk] == 1) and np.all(seen[nmk:KT] == 0) and np.all(seen[KT:] == 1)
 
 
 def test_pass_splitting(host):
@@ -146,11 +163,18 @@ def test_pass_splitting(host):
         exp = greedy(rows, seqs)
         assert [p["first"] for p in ps] == [g[0] for g in exp]
         assert [p["B"] for p in ps] == [len(g) for g in exp]
-        assert all(p["T"] <= rows for p in ps)
+        assert all(p["T"] <= up64(rows) for p in ps)
     assert [p["B"] for p in plan(host, *b.flat(), max_len=320, pass_tokens=640, max_seqs=3)] == [2, 3, 2]
     assert [p["B"] for p in plan(host, *b.flat(), max_len=320, pass_tokens=320)] == [1, 1, 2, 1, 2]
-    ps = plan(host, *b.flat(), max_len=320, max_grows=256)                 # gathered-row cap
-    assert all(p["R"] <= 256 for p in ps) and sum(p["B"] for p in ps) == 7
+    # gathered-row cap: marker rows padded to 64 plus one CLS row per question fit max_grows (at
+    # least 257, one question of 255 markers)
+    nm = [100, 90, 60, 5, 255, 64, 8]
+    b = wl.make_batch(cfg, lens, nm, seed=2)
+    ps = plan(host, *b.flat(), max_len=320, max_grows=128)
+    assert all(p["R"] <= 257 for p in ps) and sum(p["B"] for p in ps) == 7
+    # 100 + 90 -> 192 rows + 2 CLS; + 60 -> 256 + 3 > 257; 60 + 5 -> 128 + 2; + 255 > 257; 255 alone;
+    # 64 + 8 -> 128 + 2
+    assert [p["B"] for p in ps] == [2, 2, 1, 2]
 
 
 def test_config_parsing_matches_checkpoint(host, tiny_ckpt):
