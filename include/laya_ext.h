@@ -82,6 +82,22 @@ int laya_ext_gemm_split(int split_rows, int cfg_tail);
  * gathered head rows and the scorer.  Returns the previous factor, or -2 for an invalid value. */
 int laya_ext_gemm_ksplit(int ks, void* ws, size_t ws_bytes);
 
+/* laya_ext_gemm's split-K path (bf16 operands, epi 0 store or 1 fp32 residual update, as for
+ * laya_ext_gemm with laya_ext_gemm_ksplit(ksplit, ...)), allocating nothing: the fp32 partial
+ * products go to a static device array of 8 MiB that the library holds on each GPU it runs on, not
+ * to a caller's workspace.  No counterpart in the reference; it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It calls no hipMalloc, hipFree or other allocating routine; it only launches on stream (a
+ * hipStream_t) and does not wait.  Rows run in chunks whose ksplit * N fp32 partials fit the array;
+ * ksplit * N * 4 bytes above 8 MiB is rejected.  Results are bit-identical to laya_ext_gemm with the
+ * same split.  All calls on one GPU share its array: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must be serialized by the caller.  Returns 0; -1 for an
+ * unsupported shape or argument (ksplit outside 2..64, K not a multiple of 64 * ksplit, shapes
+ * laya_ext_gemm rejects); -2 when ksplit * N * 4 exceeds the array (an error is printed); -3 when
+ * the current device's array cannot be located. */
+int laya_ext_gemm_splitk_static(int epi, const void* A, const void* W, void* C, const float* bias, int act, int M,
+                                int N, int K, int ksplit, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -908,6 +908,68 @@ int laya_ext_gemm_ksplit(int ks, void* ws, size_t ws_bytes) {
   g_ext_ws_bytes = ws_bytes;
   return laya::gemm_pin_ksplit(ks);
 }
+}  // extern "C"
+
+// ---------------------------------------------------------------- split-K GEMM without allocation
+// Partial products of laya_ext_gemm_splitk_static live in this file-scope device array, one copy
+// per GPU, held until the process ends.  Host code never passes the array's name to a kernel (in
+// host code it is only a stand-in symbol): each device's address comes from hipGetSymbolAddress,
+// taken once per device with that device current, and only that address is used.
+static constexpr size_t kStaticScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+static constexpr int kMaxDevices = 64;
+static std::atomic<float*> g_scratch_ptr[kMaxDevices];
+
+// the calling thread's current device's copy of `scratch`, or null (with the error printed)
+static float* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fprintf(stderr, "[laya] laya_ext_gemm_splitk_static: no usable current device\n");
+    return nullptr;
+  }
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || addr == nullptr) {
+      fprintf(stderr, "[laya] laya_ext_gemm_splitk_static: hipGetSymbolAddress failed: %s\n", hipGetErrorString(e));
+      return nullptr;
+    }
+    p = static_cast<float*>(addr);
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+extern "C" {
+int laya_ext_gemm_splitk_static(int epi, const void* A, const void* W, void* C, const float* bias, int act, int M,
+                                int N, int K, int ksplit, void* stream) {
+  using namespace laya;
+  if ((epi != 0 && epi != 1) || ksplit < 2 || ksplit > 64 || act < 0 || act > 2) return -1;
+  GemmArgs g;
+  g.A = A; g.lda = K; g.W = W; g.ldw = K; g.M = M; g.N = N; g.K = K; g.bias = bias; g.act = act;
+  if (epi == 0) { g.C = C; g.ldc = N; } else { g.X = (float*)C; g.ldx = N; }
+  const char* why = "";
+  const int e = epi == 0 ? EPI_STORE : EPI_RESID;
+  // the split-K path of launch_gemm: the tiled kernel, K a multiple of 64 per chunk
+  if (!gemm_shape_ok(e, g, 2, &why) || gemm_planned(e, g) < 0 || K % (64 * ksplit) != 0) return -1;
+  // rows run in chunks whose ksplit x N fp32 partials fit the array; one row must fit
+  if ((size_t)ksplit * (size_t)N * sizeof(float) > kStaticScratchBytes) {
+    fprintf(stderr, "[laya] laya_ext_gemm_splitk_static: ksplit * N * 4 = %zu bytes exceeds the %zu-byte static "
+                    "scratch\n", (size_t)ksplit * N * sizeof(float), kStaticScratchBytes);
+    return -2;
+  }
+  float* ws = device_scratch();
+  if (ws == nullptr) return -3;
+  g.ksplit = ksplit;
+  g.ws = ws;
+  g.ws_bytes = kStaticScratchBytes;
+  (void)hipGetLastError();
+  launch_gemm<bf16_t>(e, g, (hipStream_t)stream);
+  LAYA_HIP(hipGetLastError());
+  return 0;
+}
+
 int laya_ext_gemm_config(int cfg) {
   if (cfg < -1 || cfg >= laya::kGemmConfigs) return -2;
   return laya::gemm_config(cfg);

@@ -26,7 +26,7 @@ ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act"
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
                "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop",
-               "laya_ext_stats", "laya_ext_attention"]
+               "laya_ext_stats", "laya_ext_attention", "laya_ext_gemm_splitk_static"]
 # every environment variable laya_create reads; Engine() sets the ones it is given for the duration
 # of laya_create only
 ENV_KNOBS = ["LAYA_PRECISION", "LAYA_MAX_TOKENS", "LAYA_PASS_TOKENS", "LAYA_MAX_SEQS", "LAYA_MAX_GATHERED",
@@ -99,6 +99,10 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p])
     L.laya_ext_attention.restype = ctypes.c_int
+    L.laya_ext_gemm_splitk_static.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_void_p]
+    L.laya_ext_gemm_splitk_static.restype = ctypes.c_int
     return L
 
 
