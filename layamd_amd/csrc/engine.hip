@@ -99,8 +99,17 @@ struct EngineIface {
 
 template <typename T>
 struct Engine : EngineIface {
-  struct EncLayer { float* attn_norm = nullptr; T* Wqkv; T* Wo; float* mlp_norm; T* Wi; T* Wmo; };
-  struct HeadLayer { float *n1w, *n1b, *n2w, *n2b, *inB, *outB, *l1B, *l2B; T *inW, *outW, *l1W, *l2W; };
+  // With the LayerNorm fold (bf16 engine), the weights read after a LayerNorm hold its weight
+  // already (rows W[n] * w) and the c_* arrays their row sums; a LayerNorm bias b is in the
+  // following GEMM's bias (bias + W . b).
+  struct EncLayer {
+    float* attn_norm = nullptr; T* Wqkv; T* Wo; float* mlp_norm; T* Wi; T* Wmo;
+    float* c_qkv = nullptr; float* c_wi = nullptr;
+  };
+  struct HeadLayer {
+    float *n1w, *n1b, *n2w, *n2b, *inB, *outB, *l1B, *l2B; T *inW, *outW, *l1W, *l2W;
+    float* c_in = nullptr; float* c_l1 = nullptr;
+  };
 
   hipStream_t stream = nullptr;
   PackLimits lim;
@@ -150,7 +159,7 @@ struct Engine : EngineIface {
 
   // measured bf16 tile configuration per (epilogue, activation, N, K, RoPE, M bucket), filled before
   // the first pass of a shape (or by tune_all); every configuration gives bit-identical results
-  using TuneKey = std::tuple<int, int, int, int, int, int>;
+  using TuneKey = std::tuple<int, int, int, int, int, int, int>;
   // a tuned launch: tile configuration, and optionally the first `split_tiles` tile rows in it and
   // the remaining rows in a second launch with configuration `tail`
   struct TilePlan { int cfg = -1, split_tiles = 0, tail = -1; };
@@ -229,6 +238,53 @@ struct Engine : EngineIface {
     LAYA_HIP(hipMemcpy(d, o.data(), o.size() * sizeof(T), hipMemcpyHostToDevice));
     return d;
   }
+  // The matrix [rows, cols] of the GEMM that reads LayerNorm(x) (weight lnw [cols], bias lnb or
+  // null) through the fold: stored row r = bf16(W[perm[r]] * lnw) (weights multiplied in fp32 and
+  // rounded once); c[r] = the sum of stored row r (exact sum of the bf16 values, rounded to fp32);
+  // bias[r] += W[perm[r]] . lnb (fp64, from the checkpoint's values) when lnb is given.
+  T* up_mat_ln(const SafeTensors& st, const std::string& n, int64_t rows, int64_t cols, const std::string& lnw_name,
+               const std::string& lnb_name, float** c_out, float** bias_io, const std::vector<int>& perm = {}) {
+    const TensorView& t = must(st, n);
+    check_shape(t, {rows, cols}, n);
+    std::vector<float> v = host_f32(t);
+    const TensorView& tw = must(st, lnw_name);
+    check_shape(tw, {cols}, lnw_name);
+    const std::vector<float> lw = host_f32(tw);
+    std::vector<float> lb;
+    if (!lnb_name.empty()) {
+      const TensorView& tb = must(st, lnb_name);
+      check_shape(tb, {cols}, lnb_name);
+      lb = host_f32(tb);
+    }
+    std::vector<T> o((size_t)(rows * cols));
+    std::vector<float> c((size_t)rows), add((size_t)rows, 0.f);
+    for (int64_t r = 0; r < rows; r++) {
+      const float* s = v.data() + (perm.empty() ? r : perm[r]) * cols;
+      T* d = o.data() + r * cols;
+      double cs = 0.0, bs = 0.0;
+      for (int64_t k = 0; k < cols; k++) {
+        d[k] = f2bf(s[k] * lw[k]);
+        cs += (double)bf2f(d[k]);
+        if (!lb.empty()) bs += (double)s[k] * (double)lb[k];
+      }
+      c[r] = (float)cs;
+      add[r] = (float)bs;
+    }
+    T* dev = dalloc<T>(o.size());
+    LAYA_HIP(hipMemcpy(dev, o.data(), o.size() * sizeof(T), hipMemcpyHostToDevice));
+    float* dc = dalloc<float>(c.size());
+    LAYA_HIP(hipMemcpy(dc, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    *c_out = dc;
+    if (!lb.empty()) {
+      // the bias (already on the device) gains W . lnb
+      std::vector<float> b((size_t)rows);
+      LAYA_HIP(hipMemcpy(b.data(), *bias_io, rows * 4, hipMemcpyDeviceToHost));
+      for (int64_t r = 0; r < rows; r++) b[r] = (float)((double)b[r] + (double)add[r]);
+      LAYA_HIP(hipMemcpy(*bias_io, b.data(), rows * 4, hipMemcpyHostToDevice));
+    }
+    return dev;
+  }
+
   // Wi rows as alternating 32-row blocks of input rows and gate rows (GeGLU epilogue pairs)
   std::vector<int> geglu_perm() const {
     const int I = cfg.intermediate;
@@ -263,14 +319,27 @@ struct Engine : EngineIface {
     final_norm = up_f32(st, "encoder.final_norm.weight", {D});
     type_emb = up_f32(st, "type_emb.weight", {3, D});
     const std::vector<int> gp = geglu_perm();
+    // With LAYA_LN_FOLD=1 the bf16 engine folds every LayerNorm that feeds a GEMM over all rows into
+    // that GEMM (see GemmArgs in kernels.h): the encoder's attn_norm (layers >= 1) and mlp_norm, the
+    // head's norm1 and, but for the last head layer (gathered rows), norm2.  Off by default: on
+    // MI355X at 9.5k rows the residual GEMMs' extra outputs (+3.5 us), the row-statistics kernels
+    // (4.8 us) and the consumers' per-element fold (+2.6 to +5 us) cost more than the 12.7 us
+    // LayerNorm kernels they replace.
+    fold_ln = sizeof(T) == 2 && D % 64 == 0 && D <= 2048 && env_int("LAYA_LN_FOLD", 0) != 0;
     enc.resize(cfg.n_layers);
     for (int i = 0; i < cfg.n_layers; i++) {
       const std::string p = "encoder.layers." + std::to_string(i) + ".";
       if (st.get(p + "attn_norm.weight") || i > 0) enc[i].attn_norm = up_f32(st, p + "attn_norm.weight", {D});
-      enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D);
+      if (fold_ln && enc[i].attn_norm)
+        enc[i].Wqkv = up_mat_ln(st, p + "attn.Wqkv.weight", 3 * D, D, p + "attn_norm.weight", "", &enc[i].c_qkv, nullptr);
+      else
+        enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D);
       enc[i].Wo = up_mat(st, p + "attn.Wo.weight", D, D);
       enc[i].mlp_norm = up_f32(st, p + "mlp_norm.weight", {D});
-      enc[i].Wi = up_mat(st, p + "mlp.Wi.weight", 2 * I, D, gp);
+      if (fold_ln)
+        enc[i].Wi = up_mat_ln(st, p + "mlp.Wi.weight", 2 * I, D, p + "mlp_norm.weight", "", &enc[i].c_wi, nullptr, gp);
+      else
+        enc[i].Wi = up_mat(st, p + "mlp.Wi.weight", 2 * I, D, gp);
       enc[i].Wmo = up_mat(st, p + "mlp.Wo.weight", D, I);
     }
     head.resize(cfg.head_layers);
@@ -279,11 +348,18 @@ struct Engine : EngineIface {
       HeadLayer& h = head[i];
       h.n1w = up_f32(st, p + "norm1.weight", {D}); h.n1b = up_f32(st, p + "norm1.bias", {D});
       h.n2w = up_f32(st, p + "norm2.weight", {D}); h.n2b = up_f32(st, p + "norm2.bias", {D});
-      h.inW = up_mat(st, p + "self_attn.in_proj_weight", 3 * D, D);
       h.inB = up_f32(st, p + "self_attn.in_proj_bias", {3 * D});
+      if (fold_ln)
+        h.inW = up_mat_ln(st, p + "self_attn.in_proj_weight", 3 * D, D, p + "norm1.weight", p + "norm1.bias", &h.c_in, &h.inB);
+      else
+        h.inW = up_mat(st, p + "self_attn.in_proj_weight", 3 * D, D);
       h.outW = up_mat(st, p + "self_attn.out_proj.weight", D, D);
       h.outB = up_f32(st, p + "self_attn.out_proj.bias", {D});
-      h.l1W = up_mat(st, p + "linear1.weight", FF, D); h.l1B = up_f32(st, p + "linear1.bias", {FF});
+      h.l1B = up_f32(st, p + "linear1.bias", {FF});
+      if (fold_ln && i + 1 < cfg.head_layers)
+        h.l1W = up_mat_ln(st, p + "linear1.weight", FF, D, p + "norm2.weight", p + "norm2.bias", &h.c_l1, &h.l1B);
+      else
+        h.l1W = up_mat(st, p + "linear1.weight", FF, D);
       h.l2W = up_mat(st, p + "linear2.weight", D, FF); h.l2B = up_f32(st, p + "linear2.bias", {D});
     }
     sc0w = up_f32(st, "scorer.0.weight", {D}); sc0b = up_f32(st, "scorer.0.bias", {D});
@@ -346,6 +422,11 @@ struct Engine : EngineIface {
     // are read by the row-wise head GEMMs, which must see finite values
     aog = dalloc<T>((size_t)RG * D, true); xng = dalloc<T>((size_t)RG * D, true); sh = dalloc<T>((size_t)RG * D, true);
     if (sizeof(T) == 2) sk_ws = dalloc<float>(kSplitKBytes / sizeof(float));
+    // LayerNorm statistics of the rows the fold's GEMMs read: [D / 64][rows][2] (group-major)
+    if (fold_ln) {
+      ln_stats = dalloc<float>((size_t)MT * (D / 64) * 2, true);
+      ln_mr = dalloc<float>((size_t)MT * 2, true);
+    }
     d_logits = dalloc<float>((size_t)RG);
     d_act = dalloc<float>((size_t)lim.max_seqs * cfg.n_act);
     d_act_hidden = dalloc<float>((size_t)lim.max_seqs * 256);
@@ -443,6 +524,9 @@ struct Engine : EngineIface {
   // many rows a batch gathered, so a row's result is the same in every batch.
   static constexpr size_t kSplitKBytes = (size_t)64 << 20;
   float* sk_ws = nullptr;
+  bool fold_ln = false;
+  float* ln_stats = nullptr;                          // per-group statistics (the residual GEMMs' scratch)
+  float* ln_mr = nullptr;                             // mean and rstd of each row of xn
   void splitk(GemmArgs& g) const {
     if (sizeof(T) != 2 || !sk_ws) return;
     g.ksplit = g.K >= 2048 ? 16 : 8;
@@ -466,7 +550,8 @@ struct Engine : EngineIface {
     return (M + step - 1) / step * step;
   }
   static TuneKey tune_key(int epi, const GemmArgs& g) {
-    return TuneKey(epi, g.act, g.N, g.K, g.rope_cos != nullptr, m_bucket(g.M));
+    return TuneKey(epi, g.act, g.N, g.K, g.rope_cos != nullptr, m_bucket(g.M),
+                   (g.ln_mr ? 1 : 0) + (g.stats ? 2 : 0) + (g.bias ? 4 : 0));
   }
 
   // one GEMM of the pass: listed while the pass is collected for tuning, otherwise launched with
@@ -596,16 +681,26 @@ struct Engine : EngineIface {
     STAGE("enc:embed_ln", launch_layernorm<T, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
                                                  nullptr, x, enc[0].attn_norm ? nullptr : xn, st));
     dump("emb", x, T_);
+    // LayerNorm fold (bf16): a residual GEMM leaves x, its bf16 copy in xn and each row's mean and rstd;
+    // the next GEMM reads xn with the LayerNorm weight folded into its own weight
+    auto fold_in = [&](GemmArgs& g, const float* c) { g.ln_mr = ln_mr; g.ln_c = c; };
+    auto fold_out = [&](GemmArgs& g) {
+      if constexpr (sizeof(T) == 2) {
+        g.Xh = xn; g.ldxh = D; g.stats = ln_stats; g.ldst = (int)MT;
+      }
+    };
     for (int L = 0; L < cfg.n_layers; L++) {
       const EncLayer& e = enc[L];
       const bool glob = cfg.global_layer[L] != 0;
-      if (L == 0 && e.attn_norm)
+      const bool last_layer = L + 1 == cfg.n_layers;
+      if (L == 0 && e.attn_norm)            // later layers' attn_norm runs after the previous layer, or is folded
         STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.attn_norm, nullptr, nullptr, nullptr,
                                                    nullptr, nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, e.Wqkv, T_, 3 * D, D, nullptr);
         g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
         g.rope_cos = glob ? cos_g : cos_l; g.rope_sin = glob ? sin_g : sin_l;
+        if (e.c_qkv && L > 0) fold_in(g, e.c_qkv);
         GSTAGE("enc:gemm_qkv_rope", gemm(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
@@ -614,28 +709,38 @@ struct Engine : EngineIface {
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
         g.X = x; g.ldx = D;
+        if (fold_ln) fold_out(g);
         GSTAGE("enc:gemm_attn_out_res", gemm(EPI_RESID, g, st));
+        if (fold_ln) STAGE("enc:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
       }
-      STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.mlp_norm, nullptr, nullptr, nullptr, nullptr,
-                                                 nullptr, xn, st));
+      if (!fold_ln)
+        STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.mlp_norm, nullptr, nullptr, nullptr, nullptr,
+                                                   nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, e.Wi, T_, 2 * I, D, nullptr);
         g.C = mg; g.ldc = I;
+        if (fold_ln) fold_in(g, e.c_wi);
         GSTAGE("enc:gemm_mlp_in_geglu", gemm(EPI_GEGLU, g, st));
       }
       {
         GemmArgs g = gemm_args(mg, I, e.Wmo, T_, D, I, nullptr);
         g.X = x; g.ldx = D;
+        if (fold_ln && !last_layer) fold_out(g);
         GSTAGE("enc:gemm_mlp_out_res", gemm(EPI_RESID, g, st));
+        if (fold_ln && !last_layer)
+          STAGE("enc:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
       }
       if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "enc%d", L); dump(nm, x, T_); }
-      if (L + 1 < cfg.n_layers) {
-        STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, enc[L + 1].attn_norm, nullptr, nullptr,
-                                                   nullptr, nullptr, nullptr, xn, st));
+      if (!last_layer) {
+        if (!fold_ln)
+          STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, enc[L + 1].attn_norm, nullptr, nullptr,
+                                                     nullptr, nullptr, nullptr, xn, st));
       } else {
-        // final_norm then + type_emb[qtype of the row's question] (ref/rl_common.py:104), in place
+        // final_norm then + type_emb[qtype of the row's question] (ref/rl_common.py:104), in place;
+        // with the fold also its bf16 copy and statistics, which the head's first GEMM reads
         STAGE("enc:final_ln_type", launch_layernorm<float, T>(x, nullptr, T_, D, eps, final_norm, nullptr, type_emb,
-                                                              d_qt, d_seq, x, (T*)nullptr, st));
+                                                              d_qt, d_seq, x, fold_ln ? xn : (T*)nullptr, st,
+                                                              fold_ln ? ln_mr : nullptr));
       }
     }
     dump("final", x, T_);
@@ -643,24 +748,32 @@ struct Engine : EngineIface {
     for (int L = 0; L < cfg.head_layers; L++) {
       const HeadLayer& hl = head[L];
       const bool last = L == cfg.head_layers - 1;
-      STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n1w, hl.n1b, nullptr, nullptr, nullptr,
-                                                  nullptr, xn, st));
+      if (!fold_ln)
+        STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n1w, hl.n1b, nullptr, nullptr, nullptr,
+                                                    nullptr, xn, st));
       {
         GemmArgs g = gemm_args(xn, D, hl.inW, T_, 3 * D, D, hl.inB);
         g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
+        if (fold_ln) fold_in(g, hl.c_in);
         GSTAGE("head:gemm_qkv", gemm(EPI_QKV, g, st));
       }
       if (!last) {
         STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt(), lim.q_tile, H, d_soff,
                                                d_vlen, nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
+          if (fold_ln) fold_out(g);
           GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
-        STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
-                                                    nullptr, xn, st));
+        if (fold_ln) STAGE("head:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
+        if (!fold_ln)
+          STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
+                                                      nullptr, xn, st));
         { GemmArgs g = gemm_args(xn, D, hl.l1W, T_, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
+          if (fold_ln) fold_in(g, hl.c_l1);
           GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
         { GemmArgs g = gemm_args(ff, FF, hl.l2W, T_, D, FF, hl.l2B); g.X = x; g.ldx = D;
+          if (fold_ln) fold_out(g);
           GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
+        if (fold_ln) STAGE("head:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
         if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards

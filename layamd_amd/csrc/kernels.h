@@ -11,11 +11,18 @@ namespace laya {
 
 // ---- LayerNorm family (one wave64 per row) ----
 // y = LN(src[row]) * w (+ b) (+ addtab[qt[seq[row]]]); src row = gather ? gather[row] : row.
-// Writes y32 (fp32, may alias x) and/or yT (storage type).  D % 4 == 0, D <= 2048.
+// Writes y32 (fp32, may alias x) and/or yT (storage type), and with ymr the mean and rstd (eps) of
+// each output row, ymr[row * 2 + {0, 1}] (what the GEMMs' LayerNorm fold reads, GemmArgs::ln_mr).
+// D % 4 == 0, D <= 2048.
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
-                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st);
+                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st,
+                      float* ymr = nullptr);
 
+// The mean and rstd (eps) of each of `rows` rows of width 64 G (G <= 32) from their per-group statistics
+// (GemmArgs::stats layout, ldst rows per group), combined in group order:
+// mr[row * 2 + {0, 1}] (GemmArgs::ln_mr).
+void launch_ln_rowstats(const float* stats, int ldst, int G, int rows, float eps, float* mr, hipStream_t st);
 // xg[r] = x[rows[r]] (fp32 rows of width D)
 void launch_gather_rows(const float* x, const int* rows, float* xg, int R, int D, hipStream_t st);
 // finite pattern in [-1, 1) over n elements (GEMM tuning operands)
@@ -52,6 +59,22 @@ struct GemmArgs {
   int ksplit = 1;
   float* ws = nullptr;
   size_t ws_bytes = 0;
+  // LayerNorm folded across two GEMMs (bf16 tiled kernel only; not with split-K).
+  //   Producer, EPI_RESID (N % 64 == 0): besides X, writes Xh [M][ldxh] = bf16 of the updated X
+  //   and, per row and 64-column group g, the group's sum and its sum of squared deviations from
+  //   the group mean, stats[(g * ldst + row) * 2 + {0, 1}] (group-major: a group's rows are
+  //   contiguous), each computed in one fixed order whatever the tile shape.  launch_ln_rowstats
+  //   then combines a row's groups into its mean and rstd.
+  //   Consumer (EPI_STORE, EPI_QKV, EPI_GEGLU): A is the producer's Xh (LayerNorm input rows) and
+  //   W holds the weight rows pre-scaled by the LayerNorm weight; with mean m and rstd r of row i
+  //   (ln_mr[i * 2 + {0, 1}]) the product becomes r * (acc - m * ln_c[n]) before bias and
+  //   activation, ln_c[n] = the sum of W's row n.  That is LN(x) w . W^T exactly in real
+  //   arithmetic; a LayerNorm bias b enters through the caller's bias (W . b).
+  bf16_t* Xh = nullptr; int ldxh = 0;
+  float* stats = nullptr;
+  int ldst = 0;                                  // rows per group in stats (>= M)
+  const float* ln_mr = nullptr;
+  const float* ln_c = nullptr;
 };
 
 template <typename T>

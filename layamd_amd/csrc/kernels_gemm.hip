@@ -618,7 +618,9 @@ __device__ __forceinline__ void xl_k_loop64d(f32x16_t (&acc)[FM][FN], const u32x
 // LOOP: the K loop.  0: two stage buffers (one workgroup per CU); 1 (128x128 tiles when the grid
 // puts two workgroups on a CU): three A buffers and two W buffers; 2 (128x128 tiles, grid of at most
 // one workgroup per CU): four stage buffers, two stages of lead.
-template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP>
+// LNX: the LayerNorm fold of GemmArgs.  With EPI_RESID the kernel writes Xh and the per-group
+// statistics; with EPI_STORE, EPI_QKV and EPI_GEGLU it applies the fold to its product.
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP, bool LNX>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   using T = bf16_t;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -645,7 +647,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // staging bytes per wave: at least a block of 32 rows x 32 fp32 columns, so every epilogue
   // stages whole 32-column accumulator blocks
   constexpr int SB = (BMP + BN) * 16 > 32 * 32 * 4 ? (BMP + BN) * 16 : 32 * 32 * 4;
-  static_assert(4 * SB + (EPI == EPI_QKV && !PRE ? 2 * BM * 32 * 4 : 0) <= NST * 16, "epilogue LDS");
+  static_assert(4 * SB + (EPI == EPI_QKV && !PRE ? 2 * BM * 32 * 4 : 0) + (LNX ? BN * 4 : 0) +
+                    (LNX && EPI == EPI_QKV ? 2 * BMP * 4 : 0) <= NST * 16,
+                "epilogue LDS");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -681,6 +685,29 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
     for (int k = 0; k < NT; k++)
       pp[k] = __builtin_amdgcn_raw_buffer_load_b32(rpos, min(m0 + ((tid + 256 * k) >> 3), a.M - 1) * 4, 0, 0);
+  }
+
+  // LayerNorm fold, consumer side: the mean and rstd of this lane's FM rows and the column sum of
+  // column n0 + tid, loaded before the first K stage is requested (the K loop's first wait then
+  // covers them: loads complete in order) and kept in registers until the epilogue
+  constexpr bool LNC = LNX && (EPI == EPI_STORE || EPI == EPI_QKV || EPI == EPI_GEGLU);
+  constexpr bool LNP = LNX && EPI == EPI_RESID;
+  static_assert(BN <= 256, "one column sum per thread");
+  float lnm[LNC ? FM : 1], lnr[LNC ? FM : 1];            // mean and rstd of rows wm WTM + 32 i + l32
+  float lnc_pre = 0.f;                                    // column sum n0 + tid (tid < BN)
+  if constexpr (LNC) {
+    // rows past M read 0
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ln_mr), (short)0,
+                                                                       a.M * 8, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (m0 + wm * WTM + 32 * i + l32) * 8, 0, 0);
+      lnm[i] = __uint_as_float(v[0]);
+      lnr[i] = __uint_as_float(v[1]);
+    }
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ln_c), (short)0,
+                                                                       (n0 + BN <= a.N ? n0 + BN : a.N) * 4, 0x00020000);
+    lnc_pre = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, (n0 + (tid < BN ? tid : 0)) * 4, 0, 0));
   }
 
   XlDma64<PA, PB> dm;
@@ -804,6 +831,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
   const int arow = wm * WTM + l32, brow = wn * WTN + l32;
   const int sw = (lane & 7) ^ ((lane >> 3) & 1);          // g(row) of fragment rows 32 n + lane % 32
+
   if constexpr (RING) {
     if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
     else xl_k_loop64r<false, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
@@ -852,6 +880,41 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   auto bias4 = [&](int n) -> float4 {
     return (a.bias && n < a.N) ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
   };
+  // LayerNorm fold: the tile's BN column sums, staged at the end of the stage memory (past the
+  // staging area and the RoPE tables); the fold r (acc - m c) is applied to each accumulator where
+  // the epilogue reads it, before bias and activation
+  float* const lcs = reinterpret_cast<float*>(L) + NST * 4 - BN;
+  // and, below them (QKV projection), the tile rows' means and rstds, which the V^T epilogue reads
+  // by row groups that differ from the accumulator layout's
+  float* const lrm = lcs - 2 * BMP;
+  if constexpr (LNC) {
+    if (tid < BN) lcs[tid] = lnc_pre;
+    if constexpr (EPI == EPI_QKV) {
+      if (wn == 0 && !hi)
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+          lrm[wm * WTM + 32 * i + l32] = lnm[i];
+          lrm[BMP + wm * WTM + 32 * i + l32] = lnr[i];
+        }
+    }
+    __syncthreads();
+  }
+  // r (acc - m c) of an accumulator of row block i
+  auto lnt = [&](float v, float c, int i) {
+    if constexpr (LNC) return __fmul_rn(fmaf(-lnm[i], c, v), lnr[i]);
+    else return v;
+  };
+  // elements 4 g .. 4 g + 3 of block (i, j) of the transposed product (row 32 i + lane % 32,
+  // columns 32 j + 8 g + 4 hi ..), fold applied
+  auto av4 = [&](int i, int j, int g) -> float4 {
+    if constexpr (LNC) {
+      const float4 c = *reinterpret_cast<const float4*>(lcs + cbase - n0 + j * 32 + 8 * g + 4 * hi);
+      return make_float4(lnt(acc[i][j][4 * g + 0], c.x, i), lnt(acc[i][j][4 * g + 1], c.y, i),
+                         lnt(acc[i][j][4 * g + 2], c.z, i), lnt(acc[i][j][4 * g + 3], c.w, i));
+    } else {
+      return make_float4(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+    }
+  };
   auto nchunks = [](int valid_elems, int per_chunk, int cpr) { return max(0, min(cpr, (valid_elems + per_chunk - 1) / per_chunk)); };
   // widest power-of-two column count <= cap that divides w
   constexpr auto fitw = [](int w, int cap) { int c = w & -w; while (c > cap) c /= 2; return c; };
@@ -871,12 +934,19 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     for (int j = 0; j < FN; j++)
 #pragma unroll
       for (int g = 0; g < 4; g++) if constexpr (HB) bb[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
+    // LayerNorm statistics of the updated rows (LNP), per 64-column group = accumulator blocks
+    // j, j + 1 (j even): each lane takes its 16 values of a block (sum, then squared deviations
+    // from their mean), combines its two blocks and then its half of the group with lane l ^ 32's
+    // (lower half first) by Chan et al.'s pairwise update, M2 = M2a + M2b + (Sb - Sa)^2 nb / (na n).
+    // The values, their order and the arithmetic do not depend on the tile shape.
+    float ls0 = 0.f, lq0 = 0.f;                           // the lane's first block of a group
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int cp = 0; cp < WTN / CW; cp++) {
 #pragma unroll
-        for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
+        for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++) {
+          float v16[16];
 #pragma unroll
           for (int g = 0; g < 4; g++) {
             float4 v;
@@ -885,12 +955,56 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
             v.z = ab(acc[i][j][4 * g + 2], bb[j][g].z);
             v.w = ab(acc[i][j][4 * g + 3], bb[j][g].w);
             *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
+            v16[4 * g + 0] = v.x; v16[4 * g + 1] = v.y; v16[4 * g + 2] = v.z; v16[4 * g + 3] = v.w;
           }
+          if constexpr (LNP) {
+            float bs = 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++) bs = __fadd_rn(bs, v16[u]);
+            const float bm = __fmul_rn(bs, 0.0625f);
+            float bq = 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+              const float d = __fsub_rn(v16[u], bm);
+              bq = fmaf(d, d, bq);
+            }
+            if ((j & 1) == 0) {
+              ls0 = bs; lq0 = bq;
+            } else {
+              const float d1 = __fsub_rn(bs, ls0);
+              const float sl = __fadd_rn(ls0, bs), ql = fmaf(__fmul_rn(d1, d1), 0.03125f, __fadd_rn(lq0, bq));
+              const float so = __shfl_xor(sl, 32, 64), qo = __shfl_xor(ql, 32, 64);
+              const float slo = hi ? so : sl, shi = hi ? sl : so, qlo = hi ? qo : ql, qhi = hi ? ql : qo;
+              const float d2 = __fsub_rn(shi, slo);
+              const float m2 = fmaf(__fmul_rn(d2, d2), 0.015625f, __fadd_rn(qlo, qhi));
+              const int row = rbase + i * 32 + l32;
+              // (a tile may extend past N; N % 64 == 0, so a group lies wholly inside or outside)
+              if (!hi && row < a.M && cbase + 32 * (j - 1) < a.N)
+                *reinterpret_cast<float2*>(a.stats + ((size_t)((cbase + 32 * (j - 1)) / 64) * a.ldst + row) * 2) =
+                    make_float2(__fadd_rn(slo, shi), m2);
+            }
+          }
+        }
         const int c0 = cbase + cp * CW;
         flush(CPR, [&](int r) -> char* {
           const int m = rbase + i * 32 + r;
           return m < a.M ? reinterpret_cast<char*>(xo + (size_t)m * a.ldx + c0) : nullptr;
         }, nchunks(a.N - c0, 4, CPR));
+        if constexpr (LNP) {
+          // the same block again as bf16 (Xh, the next GEMM's A operand)
+          constexpr int CPH = CW / 8;
+#pragma unroll
+          for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPH, ab(acc[i][j][4 * g + 0], bb[j][g].x),
+                   ab(acc[i][j][4 * g + 1], bb[j][g].y), ab(acc[i][j][4 * g + 2], bb[j][g].z),
+                   ab(acc[i][j][4 * g + 3], bb[j][g].w));
+          flush(CPH, [&](int r) -> char* {
+            const int m = rbase + i * 32 + r;
+            return m < a.M ? reinterpret_cast<char*>(a.Xh + (size_t)m * a.ldxh + c0) : nullptr;
+          }, nchunks(a.N - c0, 8, CPH));
+        }
       }
   } else if constexpr (EPI == EPI_STORE || EPI == EPI_GEGLU) {
     // bf16 rows of OW output columns, blocks of 32 rows x CW columns
@@ -917,9 +1031,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
           for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(ab(acc[i][j][4 * g + 0], bx[j][g].x)),
-                   f(ab(acc[i][j][4 * g + 1], bx[j][g].y)), f(ab(acc[i][j][4 * g + 2], bx[j][g].z)), f(ab(acc[i][j][4 * g + 3], bx[j][g].w)));
+            for (int g = 0; g < 4; g++) {
+              const float4 v = av4(i, j, g);
+              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(ab(v.x, bx[j][g].x)), f(ab(v.y, bx[j][g].y)),
+                   f(ab(v.z, bx[j][g].z)), f(ab(v.w, bx[j][g].w)));
+            }
         } else {
           // 64-column groups [input 32 | gate 32] (blocks jp, jp + 1) -> output column (c / 64) * 32 + c % 64
 #pragma unroll
@@ -927,11 +1043,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
             for (int g = 0; g < 4; g++) {
               const float4 x = bx[jp][g], y = bx[jp + 1][g];
-              const f32x16_t& p = acc[i][jp];
-              const f32x16_t& q = acc[i][jp + 1];
-              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(ab(p[4 * g + 0], x.x)) * ab(q[4 * g + 0], y.x),
-                   gelu_erf_as(ab(p[4 * g + 1], x.y)) * ab(q[4 * g + 1], y.y), gelu_erf_as(ab(p[4 * g + 2], x.z)) * ab(q[4 * g + 2], y.z),
-                   gelu_erf_as(ab(p[4 * g + 3], x.w)) * ab(q[4 * g + 3], y.w));
+              const float4 p = av4(i, jp, g), q = av4(i, jp + 1, g);
+              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(ab(p.x, x.x)) * ab(q.x, y.x),
+                   gelu_erf_as(ab(p.y, x.y)) * ab(q.y, y.y), gelu_erf_as(ab(p.z, x.z)) * ab(q.z, y.z),
+                   gelu_erf_as(ab(p.w, x.w)) * ab(q.w, y.w));
             }
         }
         const int c0 = ocol + cp * CW;
@@ -989,10 +1104,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
             for (int g = 0; g < 4; g++) {
               const int dd = 8 * g + 4 * hi;
               const float4 x0 = bx[jp][g], x1 = bx[jp + 1][g];
-              const float p1[4] = {ab(acc[i][jp][4 * g + 0], x0.x), ab(acc[i][jp][4 * g + 1], x0.y), ab(acc[i][jp][4 * g + 2], x0.z),
-                                   ab(acc[i][jp][4 * g + 3], x0.w)};
-              const float p2[4] = {ab(acc[i][jp + 1][4 * g + 0], x1.x), ab(acc[i][jp + 1][4 * g + 1], x1.y),
-                                   ab(acc[i][jp + 1][4 * g + 2], x1.z), ab(acc[i][jp + 1][4 * g + 3], x1.w)};
+              const float4 a1 = av4(i, jp, g), a2 = av4(i, jp + 1, g);
+              const float p1[4] = {ab(a1.x, x0.x), ab(a1.y, x0.y), ab(a1.z, x0.z), ab(a1.w, x0.w)};
+              const float p2[4] = {ab(a2.x, x1.x), ab(a2.y, x1.y), ab(a2.z, x1.z), ab(a2.w, x1.w)};
               float o1[4], o2[4];
               if (rope) {
                 // rotate_half partners (d, d + 32) of a head are blocks jp, jp + 1 of one lane
@@ -1023,18 +1137,38 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       // [column][row] blocks of 32 columns x CW rows, streamed out along rows of V^T (chunks that
       // start past row M are not written)
       constexpr int CW = fitw(WTM, SB / 64), CPR = CW / 8;
+      float bvs[FN];                                       // loaded before the first store
 #pragma unroll
       for (int j = 0; j < FN; j++) {
         const int n = cbase + j * 32 + l32;
-        const float bv = HB && a.bias && n < a.N ? a.bias[n] : 0.f;
+        bvs[j] = HB && a.bias && n < a.N ? a.bias[n] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const float bv = bvs[j];
+        const float cv = LNC ? lcs[cbase - n0 + j * 32 + l32] : 0.f;
 #pragma unroll
         for (int cp = 0; cp < WTM / CW; cp++) {
 #pragma unroll
           for (int i = cp * CW / 32; i < (cp + 1) * CW / 32; i++)
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, ab(acc[i][j][4 * g + 0], bv), ab(acc[i][j][4 * g + 1], bv),
-                   ab(acc[i][j][4 * g + 2], bv), ab(acc[i][j][4 * g + 3], bv));
+            for (int g = 0; g < 4; g++) {
+              // element 4 g + u is row 32 i + 8 g + 4 hi + u of the wave's tile part; that row's mean
+              // and rstd come from the table
+              float v[4];
+#pragma unroll
+              for (int u = 0; u < 4; u++) v[u] = acc[i][j][4 * g + u];
+              if constexpr (LNC) {
+                const int r4 = wm * WTM + 32 * i + 8 * g + 4 * hi;
+                const float4 m4 = *reinterpret_cast<const float4*>(lrm + r4);
+                const float4 q4 = *reinterpret_cast<const float4*>(lrm + BMP + r4);
+                v[0] = __fmul_rn(fmaf(-m4.x, cv, v[0]), q4.x);
+                v[1] = __fmul_rn(fmaf(-m4.y, cv, v[1]), q4.y);
+                v[2] = __fmul_rn(fmaf(-m4.z, cv, v[2]), q4.z);
+                v[3] = __fmul_rn(fmaf(-m4.w, cv, v[3]), q4.w);
+              }
+              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, ab(v[0], bv), ab(v[1], bv), ab(v[2], bv), ab(v[3], bv));
+            }
           const int r0 = rbase + cp * CW;
           flush(CPR, [&](int rr) -> char* {
             const int nn = cbase + j * 32 + rr;
@@ -1101,10 +1235,43 @@ static int num_cus() {
   return n;
 }
 
+// whether a launch uses the LayerNorm fold (GemmArgs), and whether this kernel set has it: the
+// residual update (with or without bias), the QKV projection, GeGLU without bias and a ReLU store
+// with bias, the epilogues the engine folds a LayerNorm into
+static bool ln_fold(const GemmArgs& a) { return a.ln_mr != nullptr || a.stats != nullptr || a.Xh != nullptr; }
+
+template <int EPI, int ACT>
+static constexpr bool ln_fold_built(bool bias) {
+  return EPI == EPI_RESID || EPI == EPI_QKV || (EPI == EPI_GEGLU && ACT == ACT_NONE) || (EPI == EPI_STORE && ACT == ACT_RELU);
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, int ACT, int LOOP>
 static void launch_xl_ring(const GemmArgs& a, int tiles, hipStream_t st) {
-  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP>), dim3(tiles), dim3(256), 0, st, a);
-  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP>), dim3(tiles), dim3(256), 0, st, a);
+  if (ln_fold(a)) {
+    // (256x256 fold consumers are not built: they would spill; xl_cfg_fits never offers them)
+    if constexpr (ln_fold_built<EPI, ACT>(true) && (EPI == EPI_RESID || BM * BN < 256 * 256)) {
+      const bool hb = EPI == EPI_QKV || a.bias != nullptr;
+      if constexpr (EPI == EPI_RESID) {
+        if (hb) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        return;
+      } else if constexpr (EPI == EPI_QKV) {
+        // the encoder's projection has no bias; its fold kernel leaves the bias code out
+        if (a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        return;
+      } else if constexpr (EPI == EPI_STORE) {
+        if (hb) { hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
+      } else {
+        if (!hb) { hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
+      }
+    }
+    fprintf(stderr, "[laya] gemm: no LayerNorm-fold kernel for epilogue %d, activation %d, bias %d\n", EPI, ACT,
+            (int)(a.bias != nullptr));
+    exit(1);
+  }
+  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
+  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
 }
 
 // 128x128 tiles take the three-A-buffer loop when the grid has more tiles than the chip has CUs,
@@ -1191,6 +1358,18 @@ bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) 
     if (a.N != 3 * a.H * a.HD || a.HD % 16) { *why = "QKV needs N == 3*H*HD, HD % 16 == 0"; return false; }
     if (a.rope_cos && a.HD != 64) { *why = "fused RoPE needs HD == 64"; return false; }
   }
+  if (ln_fold(a)) {
+    if (elt_bytes != 2 || a.ksplit > 1) { *why = "the LayerNorm fold needs bf16 operands and no split-K"; return false; }
+    if (a.ln_mr && (epi == EPI_RESID || epi == EPI_PARTIAL || !a.ln_c)) {
+      *why = "LayerNorm-fold consumers: store, QKV or GeGLU epilogue with column sums";
+      return false;
+    }
+    const bool prod = a.stats || a.Xh;
+    if (prod && (epi != EPI_RESID || !a.stats || !a.Xh || a.N % 64 || a.ldxh % 8 || a.ldxh < a.N || a.ldst < a.M)) {
+      *why = "LayerNorm-fold producers: residual epilogue with Xh and statistics, N a multiple of 64, ldst >= M";
+      return false;
+    }
+  }
   return true;
 }
 
@@ -1205,6 +1384,8 @@ static bool xl_usable(int epi, const GemmArgs& a) {
 
 static bool xl_cfg_fits(int epi, const GemmArgs& a, int cfg) {
   if (cfg < 0 || cfg >= kGemmConfigs) return false;
+  // the LayerNorm-fold consumers do not fit 256x256 tiles' registers (they would spill)
+  if (a.ln_mr && cfg == 0) return false;
   return epi != EPI_QKV || (kXl[cfg].bm <= kXl[cfg].bn && (a.H * a.HD) % kXl[cfg].bn == 0);
 }
 
@@ -1239,6 +1420,9 @@ static GemmArgs rows_from(const GemmArgs& a, int r0) {
   b.A = reinterpret_cast<const bf16_t*>(a.A) + (size_t)r0 * a.lda;
   if (a.C) b.C = reinterpret_cast<bf16_t*>(a.C) + (size_t)r0 * a.ldc;
   if (a.X) b.X = a.X + (size_t)r0 * a.ldx;
+  if (a.Xh) b.Xh = a.Xh + (size_t)r0 * a.ldxh;
+  if (a.stats) b.stats = a.stats + (size_t)r0 * 2;
+  if (a.ln_mr) b.ln_mr = a.ln_mr + (size_t)r0 * 2;
   if (a.Q) b.Q = reinterpret_cast<bf16_t*>(a.Q) + (size_t)r0 * a.ldqk;
   if (a.Kt) b.Kt = reinterpret_cast<bf16_t*>(a.Kt) + (size_t)r0 * a.ldqk;
   if (a.Vt) b.Vt = reinterpret_cast<bf16_t*>(a.Vt) + r0;
@@ -1356,9 +1540,13 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     fprintf(stderr, "[laya] gemm %dx%dx%d epi %d rejected: %s\n", a.M, a.N, a.K, epi, why);
     exit(1);
   }
+  if (ln_fold(a) && (sizeof(T) != 2 || !xl_usable(epi, a) || gemm_planned(epi, a) < 0)) {
+    fprintf(stderr, "[laya] gemm %dx%dx%d epi %d: the LayerNorm fold needs the tiled bf16 kernel\n", a.M, a.N, a.K, epi);
+    exit(1);
+  }
   if constexpr (sizeof(T) == 2) {
     if (xl_usable(epi, a)) {
-      const int pinned_ks = g_ksplit.load(std::memory_order_relaxed);
+      const int pinned_ks = ln_fold(a) ? 0 : g_ksplit.load(std::memory_order_relaxed);
       const int ks = a.ksplit > 1 ? a.ksplit : pinned_ks;
       if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % (ks * 64) == 0 && a.ws != nullptr) {
         launch_splitk(epi, a, ks, st);

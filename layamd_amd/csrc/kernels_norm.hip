@@ -4,6 +4,7 @@
 // registers (D/256 float4 per lane and row), reduces mean and variance with wave shuffles (no
 // LDS, no barriers), and writes the normalised rows in one pass.  Four waves per workgroup.
 #include "kernels.h"
+#include <type_traits>
 
 namespace laya {
 
@@ -34,12 +35,12 @@ template <> struct St4<bf16_t> {
 
 // Each wave normalises RPW rows; all of their loads are issued before the first reduction so
 // every lane keeps 4*RPW 16-byte loads in flight.
-template <typename Tin, typename T, int RPW, int NCH>
+template <typename Tin, typename T, int RPW, int NCH, bool MR>
 __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __restrict__ gather, int rows, int D,
                                                    float eps, const float* __restrict__ w, const float* __restrict__ b,
                                                    const float* __restrict__ addtab, const int* __restrict__ qt,
                                                    const int* __restrict__ seq, float* y32,  // may alias x
-                                                   T* __restrict__ yT) {
+                                                   T* __restrict__ yT, float* __restrict__ ymr) {
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   const int nc = D >> 2;
@@ -79,6 +80,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
     }
     const float inv = rsqrtf(wave_sum(qq) / D + eps);
     const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
+    float4 ov[MR ? NCH : 1];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
@@ -90,7 +92,25 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
         if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[c]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
         if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[c] = o;
         if (yT) St4<T>::at(yT + (size_t)row * D, c, o);
+        if constexpr (MR) ov[j] = o;
       }
+    }
+    if constexpr (MR) {
+      // mean and rstd of the output row (two passes over the values kept in registers)
+      float os = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCH; j++)
+        if (lane + 64 * j < nc) os += (ov[j].x + ov[j].y) + (ov[j].z + ov[j].w);
+      const float om = wave_sum(os) / D;
+      float oq = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCH; j++)
+        if (lane + 64 * j < nc) {
+          const float a = ov[j].x - om, bb = ov[j].y - om, cc = ov[j].z - om, d = ov[j].w - om;
+          oq += (a * a + bb * bb) + (cc * cc + d * d);
+        }
+      const float orr = rsqrtf(wave_sum(oq) / D + eps);
+      if (lane == 0) reinterpret_cast<float2*>(ymr)[row] = make_float2(om, orr);
     }
   }
 }
@@ -101,25 +121,75 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
 // reductions (125 VGPRs, half the occupancy) both measured slower there.
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
-                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st) {
-  if (D % 4 || D > kLnMaxChunks * 256) { fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D); exit(1); }
-  if (rows <= 0) return;
-  if (D <= 1024) {
-    constexpr int RPW = 2;
-    hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x, gather,
-                       rows, D, eps, w, b, addtab, qt, seq, y32, yT);
-  } else {
-    hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows, D, eps, w, b,
-                       addtab, qt, seq, y32, yT);
+                      const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st,
+                      float* ymr) {
+  if (D % 4 || D > kLnMaxChunks * 256) {
+    fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D);
+    exit(1);
   }
+  if (rows <= 0) return;
+  auto go = [&](auto mr) {
+    constexpr bool MR = decltype(mr)::value;
+    if (D <= 1024) {
+      constexpr int RPW = 2;
+      hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4, MR>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x,
+                         gather, rows, D, eps, w, b, addtab, qt, seq, y32, yT, ymr);
+    } else {
+      hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks, MR>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows,
+                         D, eps, w, b, addtab, qt, seq, y32, yT, ymr);
+    }
+  };
+  if (ymr) go(std::true_type{});
+  else go(std::false_type{});
 }
 
 template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
-                                             const float*, const int*, const int*, float*, float*, hipStream_t);
+                                             const float*, const int*, const int*, float*, float*, hipStream_t, float*);
 template void launch_layernorm<float, bf16_t>(const float*, const int*, int, int, float, const float*, const float*,
-                                              const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
+                                              const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*);
 template void launch_layernorm<bf16_t, bf16_t>(const bf16_t*, const int*, int, int, float, const float*, const float*,
-                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t);
+                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*);
+
+// One thread per row: the G group pairs (sum, M2) of the row are read group-major (a group's rows
+// are contiguous, so a wave's reads of one group are coalesced), all at once for up to 16 groups,
+// and combined in group order, M2 = sum over g of (M2_g + (S_g - 64 mean)^2 / 64) (Chan et al.'s
+// update for equal group sizes).
+template <int GB>
+__global__ __launch_bounds__(64) void k_ln_rowstats(const float2* __restrict__ stats, int ldst, int G, int rows,
+                                                    float eps, float2* __restrict__ mr) {
+  const int row = blockIdx.x * 64 + threadIdx.x;
+  if (row >= rows) return;
+  float2 p[GB];
+#pragma unroll
+  for (int g = 0; g < GB; g++) p[g] = g < G ? stats[(size_t)g * ldst + row] : make_float2(0.f, 0.f);
+  const float invn = 1.0f / (64.f * (float)G);
+  float sum = 0.f;
+#pragma unroll
+  for (int g = 0; g < GB; g++)
+    if (g < G) sum = __fadd_rn(sum, p[g].x);
+  const float mean = __fmul_rn(sum, invn);
+  float m2 = 0.f;
+#pragma unroll
+  for (int g = 0; g < GB; g++)
+    if (g < G) {
+      const float d = fmaf(-64.f, mean, p[g].x);          // group sum - 64 mean
+      m2 = __fadd_rn(m2, fmaf(__fmul_rn(d, d), 0.015625f, p[g].y));
+    }
+  mr[row] = make_float2(mean, rsqrtf(fmaf(m2, invn, eps)));
+}
+
+void launch_ln_rowstats(const float* stats, int ldst, int G, int rows, float eps, float* mr, hipStream_t st) {
+  if (G < 1 || G > 32 || ldst < rows) {
+    fprintf(stderr, "[laya] ln_rowstats: %d groups, %d rows per group for %d rows\n", G, ldst, rows);
+    exit(1);
+  }
+  if (rows <= 0) return;
+  auto* sp = reinterpret_cast<const float2*>(stats);
+  auto* mp = reinterpret_cast<float2*>(mr);
+  // one wave per workgroup: the few hundred waves spread over as many CUs
+  if (G <= 16) hipLaunchKernelGGL(k_ln_rowstats<16>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
+  else hipLaunchKernelGGL(k_ln_rowstats<32>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
+}
 
 // Deterministic finite pattern, uniform in [-1, 1), written over n elements (operands for GEMM
 // tuning runs, which must see realistic MFMA power and produce finite results).

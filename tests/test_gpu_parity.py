@@ -51,7 +51,7 @@ BF16_PROB = 1e-3
 # for laya_create only, so nothing leaks from one engine to the next)
 ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
        "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
-       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None}
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None}
 _ENGINES = {}
 
 
@@ -536,6 +536,34 @@ def test_attention_query_tiles_bit_identical():
         assert np.array_equal(lo128, lo64) and np.array_equal(ac128, ac64), tag
 
 
+def test_ln_fold_bits():
+    """The LayerNorm fold (LAYA_LN_FOLD=1) keeps the engine's bit properties: graph replays equal the
+    eager pass, and every tile configuration the fold's GEMMs can use (the 256x256 consumers are not
+    built; a pinned configuration 0 leaves them on their tuned one) gives the same bits, on 12 questions
+    of the b32 x s512 batch on ModernBERT-large (2 head layers: both folds of the head run)."""
+    b = wl.c3(0).subset(list(range(12)))
+    e = engine("large", "bf16", LAYA_GRAPHS=0, LAYA_LN_FOLD=1)
+    ref_lo, ref_ac = e.forward_flat(*b.flat())
+    assert np.isfinite(ref_lo).all() and np.isfinite(ref_ac).all()
+    g = engine("large", "bf16", LAYA_LN_FOLD=1)
+    for _ in range(3):
+        lo, ac = g.forward_flat(*b.flat())
+        assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac)
+    prev = le.gemm_config(e.lib, -1)
+    try:
+        for cfg in (0, 1, 3, 4, 5, 7, 8):
+            le.gemm_config(e.lib, cfg)
+            lo, ac = e.forward_flat(*b.flat())
+            assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
+    finally:
+        le.gemm_config(e.lib, prev)
+    # against the unfolded engine: the same model within the bf16 probability bar
+    lo0, _ = engine("large", "bf16", LAYA_GRAPHS=0).forward_flat(*b.flat())
+    dp = prob_delta(ref_lo, lo0, b.nmark)
+    print("fold vs unfolded: dprob %.5f, dlogit %.5f" % (dp, float(np.abs(ref_lo - lo0).max())))
+    assert dp < BF16_PROB
+
+
 def test_gemm_tuning_keeps_outputs():
     """laya_tune_all times every tile configuration of every GEMM bucket up to the pass capacity, as
     the reference tunes its GEMM plans per M bucket (src/engine.hip:295-379).  All configurations
@@ -588,30 +616,35 @@ def test_bf16_sample_layer_drift(tag):
     ref_lo, ref_ac, caps = om.run_per_question(om.Weights(W), ck.PRESETS[preset], b, capture_rows=True)
     lens, ids, nm, mk, qt = b.flat()
     soff = np.concatenate([[0], np.cumsum((lens + 7) // 8 * 8)])
-    worst = (0.0, "")
-    with tempfile.TemporaryDirectory() as dd:
-        e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0))
-        lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
-        for li, name in enumerate(ref["layers"]):
-            got = _dump_rows(dd, {"final_norm": "final"}.get(str(name), str(name)), cfg.d)
-            for i in range(b.B):
-                r = caps[i][str(name)]
-                gi = got[soff[i]:soff[i] + lens[i]].astype(np.float64)
-                if name == "final_norm":
-                    gi = gi - W["type_emb.weight"][qt[i]]
-                eng, up = _rel_drift(gi, r), float(ref["rel_drift_bf16_autocast"][li, i])
-                worst = max(worst, (eng / (BF16_VS_UPSTREAM * up + BF16_FLOOR_REL), "%s q%d" % (name, i)))
-                if i == 0 or eng > BF16_VS_UPSTREAM * up + BF16_FLOOR_REL:
-                    print("%s bf16 %-10s q%d engine %.4f reference-bf16 %.4f" % (tag, name, i, eng, up))
-                assert eng <= BF16_VS_UPSTREAM * up + BF16_FLOOR_REL, (name, i, eng, up)
-    print("%s bf16 worst layer drift / budget %.3f (%s)" % (tag, worst[0], worst[1]))
     up_lo = np.concatenate([ref["logits_bf16_autocast"][i, :nm[i]] - ref["logits"][i, :nm[i]] for i in range(b.B)])
-    dl, dl_up = float(np.abs(lo - ref_lo).max()), float(np.abs(up_lo).max())
-    da, da_up = float(np.abs(ac - ref_ac).max()), float(np.abs(ref["act_logits_bf16_autocast"] - ref["act_logits"]).max())
-    print("%s bf16 dlogit engine %.5f reference-bf16 %.5f; dact engine %.5f reference-bf16 %.5f; dprob %.5f"
-          % (tag, dl, dl_up, da, da_up, prob_delta(lo, ref_lo, nm)))
-    assert dl <= BF16_VS_UPSTREAM * dl_up + BF16_FLOOR_LOGIT
-    assert da <= BF16_VS_UPSTREAM * da_up + BF16_FLOOR_LOGIT
+    dl_up = float(np.abs(up_lo).max())
+    da_up = float(np.abs(ref["act_logits_bf16_autocast"] - ref["act_logits"]).max())
+    # the c3 sample also runs the LayerNorm fold (LAYA_LN_FOLD=1), against the same budgets
+    for fold in ((0, 1) if tag == "c3_sample" else (0,)):
+        worst = (0.0, "")
+        with tempfile.TemporaryDirectory() as dd:
+            e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0, LAYA_LN_FOLD=fold))
+            lo_f, ac_f = e.forward_flat(lens, ids, nm, mk, qt)
+            for li, name in enumerate(ref["layers"]):
+                got = _dump_rows(dd, {"final_norm": "final"}.get(str(name), str(name)), cfg.d)
+                for i in range(b.B):
+                    r = caps[i][str(name)]
+                    gi = got[soff[i]:soff[i] + lens[i]].astype(np.float64)
+                    if name == "final_norm":
+                        gi = gi - W["type_emb.weight"][qt[i]]
+                    eng, up = _rel_drift(gi, r), float(ref["rel_drift_bf16_autocast"][li, i])
+                    worst = max(worst, (eng / (BF16_VS_UPSTREAM * up + BF16_FLOOR_REL), "%s q%d" % (name, i)))
+                    if i == 0 or eng > BF16_VS_UPSTREAM * up + BF16_FLOOR_REL:
+                        print("%s bf16 fold=%d %-10s q%d engine %.4f reference-bf16 %.4f" % (tag, fold, name, i, eng, up))
+                    assert eng <= BF16_VS_UPSTREAM * up + BF16_FLOOR_REL, (fold, name, i, eng, up)
+        print("%s bf16 fold=%d worst layer drift / budget %.3f (%s)" % (tag, fold, worst[0], worst[1]))
+        dl, da = float(np.abs(lo_f - ref_lo).max()), float(np.abs(ac_f - ref_ac).max())
+        print("%s bf16 fold=%d dlogit engine %.5f reference-bf16 %.5f; dact engine %.5f reference-bf16 %.5f; dprob %.5f"
+              % (tag, fold, dl, dl_up, da, da_up, prob_delta(lo_f, ref_lo, nm)))
+        assert dl <= BF16_VS_UPSTREAM * dl_up + BF16_FLOOR_LOGIT, fold
+        assert da <= BF16_VS_UPSTREAM * da_up + BF16_FLOOR_LOGIT, fold
+        if fold == 0:
+            lo, ac = lo_f, ac_f
     if tag == "c5_sample":
         e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=32768))
         flo, fac = e.forward_flat(*full.flat())

@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 
 ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
        "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
-       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None}
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None}
 
 
 def make_engine(model_dir, precision, **env):
