@@ -33,15 +33,28 @@ template <> struct Elt<bf16_t> {
   static __device__ __forceinline__ void st(bf16_t* p, float v) { *p = f2bf(v); }
 };
 
+// Wave64 reductions (all 64 lanes active): within each 16-lane row by DPP (quad_perm xor 1,
+// quad_perm xor 2, row_half_mirror, row_mirror: each step pairs lanes whose values are equal
+// within their groups, so every lane of a row ends with the same row total), then the four row
+// totals read as scalars and combined as (r0 + r1) + (r2 + r3).  No LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f32<0xB1>(v);                                  // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);                                  // quad_perm [2, 3, 0, 1]
+  v += dpp_f32<0x141>(v);                                 // row_half_mirror
+  v += dpp_f32<0x140>(v);                                 // row_mirror
+  return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 // exact (erf) GELU, as torch.nn.functional.gelu with approximate="none"

@@ -21,6 +21,8 @@
 // layers, |p - j| <= window_half (inclusive, HF masking_utils.py:141-151).  Keys beyond the
 // sequence are read (V^T columns up to the next 64-key boundary exist and hold finite values:
 // padding rows, the next question, or the zero-initialised slack) but get probability exactly 0.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace laya {
@@ -236,13 +238,14 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 //   S^T[key][query] = K Q^T   A = K rows (32 keys x 16 d per MFMA), B = Q rows (registers)
 //   O^T[d][query] += V^T P^T  A = V^T rows (32 d x 16 keys),       B = P^T from the S^T registers
 //
-// The 32x32 accumulator gives lane l query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of a
-// 32-key sub-block, so lanes l and l ^ 32 together hold a query's 64 scores: the row max takes one
-// cross-lane step, and the row sum is one more MFMA per PV step (an all-ones A operand times P^T).
-// Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand
-// of one 16-key PV step with k-index i <-> key 16 h' + 8 (i / 4) + 4 (l / 32) + i % 4; the V^T
-// operand reads the same keys (two 8-byte pieces per lane).  Scores are scaled into the log2
-// domain once (exp2); blocks whose keys are all visible to every query of the tile skip the mask.
+// The 32x32 accumulator gives lane l query l % 32 and rows 8 (e / 4) + 4 (l / 32) + e % 4 of a
+// 32-key sub-block; the K operand's rows are permuted so that these rows are keys
+// 16 (e / 8) + 8 (l / 32) + e % 8.  Lanes l and l ^ 32 together hold a query's 64 scores: the row
+// max takes one cross-lane step, and the row sum is one more MFMA per PV step (an all-ones A operand
+// times P^T).  Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand of one 16-key PV
+// step with k-index i <-> key 16 h' + i, so the V^T operand of that step is one 16-byte LDS read per
+// lane.  Scores are scaled into the log2 domain once (exp2).  Global layers' blocks but the last
+// partial one skip the mask; sliding-window blocks all take it.
 // ======================================================================================
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -299,15 +302,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   if (gq) { const int gi = gq[tile.q0 + rr]; p = grow[gi] - base; orow = gi; }
   else { p = tile.q0 + rr; orow = base + p; }
 
-  // key range of the tile and the range whose blocks need no mask
+  // key range of the tile
   int lo = 0, hi_k = len;
-  int full_lo = 0, full_hi = len;                         // keys visible to every query of the tile
   if (window_half > 0 && !gq) {
     const int pmin = tile.q0, pmax = tile.q0 + tile.nq - 1;
     lo = max(0, pmin - window_half) & ~15;
     hi_k = min(len, pmax + window_half + 1);
-    full_lo = pmax - window_half;
-    full_hi = min(len, pmin + window_half + 1);
   }
 
   // keys visible to this lane's query: [jlo, jhi)
@@ -369,17 +369,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  const int sw = (l32 >> 1) & 7;                           // swizzle of fragment rows 32 n + l32
-  int it = 0;
-  for (int k0 = lo; k0 < hi_k; k0 += 64, ++it) {
-    const bool odd = it & 1;
-    const u32x4_t* ks = odd ? Ks1 : Ks0;
-    const u32x4_t* vs = Vs;
-    const bool more = k0 + 64 < hi_k;
-    // the other K buffer was last read by the previous block's scores, before its final barrier
-    if (more) fetch_k(k0 + 64, odd ? Ks0 : Ks1);
-
-    // ---- S^T = K Q^T: two 32-key sub-blocks ----
+  // Key order of the score MFMA: its A row m (lane m of the K operand) is key pk(m) of the 32-key
+  // sub-block, pk(8 a + 4 h + c) = 16 (a / 2) + 8 h + 4 (a % 2) + c.  Score element e of lane l
+  // then holds key 16 (e / 8) + 8 (l / 32) + e % 8, so the eight elements that form the B operand
+  // of a 16-key PV step are the eight consecutive keys at k-indices 8 (l / 32) .. + 7, and the V^T
+  // operand of that step is one 16-byte chunk of each d row.
+  const int krow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
+  const int ksw = (krow >> 1) & 7;                         // swizzle of K rows 32 n + krow
+  // One 64-key block: S^T = K Q^T, online softmax (MASKED: with the per-query key range), O^T +=
+  // V^T P^T.  The masked and unmasked blocks are separate copies of the whole block, so that the
+  // scores go from the MFMA to the softmax in the registers the MFMA wrote them to.
+  auto block = [&](auto masked, int k0, bool more, const u32x4_t* ks) {
+    constexpr bool MASKED = decltype(masked)::value;
     f32x16_t st[2];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
@@ -387,31 +388,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
       for (int e = 0; e < 16; e++) st[kb][e] = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        const u32x4_t kf = ks[(32 * kb + l32) * 8 + ((2 * s + hi) ^ sw)];
+        const u32x4_t kf = ks[(32 * kb + krow) * 8 + ((2 * s + hi) ^ ksw)];
         st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
                                                          __builtin_bit_cast(bf16x8_t, qf[s]), st[kb], 0, 0, 0);
       }
     }
-
-    // ---- mask, online softmax (branch-free per lane) ----
-    const bool full = k0 >= full_lo && k0 + 64 <= full_hi;
     float mx = -INFINITY;
-    if (full) {
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) mx = fmaxf(mx, st[kb][e]);
-    } else {
-      // visible keys of this lane's query: [jlo, jhi)
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int j = k0 + 32 * kb + 8 * (e >> 2) + 4 * hi + (e & 3);
+      for (int e = 0; e < 16; e++) {
+        if constexpr (MASKED) {
+          // visible keys of this lane's query: [jlo, jhi)
+          const int j = k0 + 32 * kb + 16 * (e >> 3) + 8 * hi + (e & 7);
           st[kb][e] = (unsigned)(j - jlo) < (unsigned)(jhi - jlo) ? st[kb][e] : -INFINITY;
-          mx = fmaxf(mx, st[kb][e]);
         }
-    }
+        mx = fmaxf(mx, st[kb][e]);
+      }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
     // with no visible key yet (m_new = -inf) every exp2 below is exp2(-inf) = 0
@@ -432,8 +425,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     }
     m_run = m_new;
 
-    // this block's V^T (fetched after the previous PV step, before the K fetch above) has landed
-    // in every wave's part
+    // this block's V^T (fetched after the previous PV step, before the K fetch) has landed in
+    // every wave's part
     if (more) {
       if constexpr (J == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
@@ -443,7 +436,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
-    // ---- O^T += V^T P^T: four 16-key steps ----
+    // ---- O^T += V^T P^T: four 16-key steps; step kk covers keys 16 kk + 8 hi + (0..7) in lane l ----
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
       const f32x16_t& sp = st[kk >> 1];
@@ -454,20 +447,39 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 #pragma unroll
       for (int db = 0; db < 2; db++) {
         const int d = 32 * db + l32;
-        const u32x2_t* vrow = reinterpret_cast<const u32x2_t*>(vs + d * 8);
-        // keys 16 kk + 4 hi + (0..3): chunk 2 kk, half hi; keys 16 kk + 8 + 4 hi + (0..3): chunk 2 kk + 1
-        const u32x2_t u0 = vrow[2 * ((2 * kk) ^ ((d >> 1) & 7)) + hi];
-        const u32x2_t u1 = vrow[2 * ((2 * kk + 1) ^ ((d >> 1) & 7)) + hi];
-        const u32x4_t va = (u32x4_t){u0.x, u0.y, u1.x, u1.y};
+        const u32x4_t va = Vs[d * 8 + ((2 * kk + hi) ^ ((d >> 1) & 7))];
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pb, o[db], 0, 0, 0);
       }
       lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb, lsum, 0, 0, 0);
     }
+  };
+
+  // One pass of the loop below: the block at k0 (K in buffer `it` % 2), then the fetches of the
+  // next one.  Each call site of `block` holds its own copy of the whole block (no score register
+  // is shared between the masked and the unmasked copy).
+  int it = 0, k0 = lo;
+  auto step = [&](auto masked) {
+    const bool odd = it & 1;
+    const u32x4_t* ks = odd ? Ks1 : Ks0;
+    const bool more = k0 + 64 < hi_k;
+    // the other K buffer was last read by the previous block's scores, before its final barrier
+    if (more) fetch_k(k0 + 64, odd ? Ks0 : Ks1);
+    block(masked, k0, more, ks);
     // the next block's K has landed (this wave's part) and no wave still reads V^T or this K
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (more) fetch_v(k0 + 64);
+    k0 += 64;
+    ++it;
+  };
+  if (window_half > 0 && !gq) {
+    // sliding window: a tile's few blocks are mostly partly visible; all take the mask
+    while (k0 < hi_k) step(std::true_type{});
+  } else {
+    // global: every block but the last partial one is visible to every query
+    while (k0 + 64 <= hi_k) step(std::false_type{});
+    if (k0 < hi_k) step(std::true_type{});
   }
 
   if (!qvalid) return;

@@ -44,6 +44,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   const int nc = D >> 2;
+  const float invd = 1.0f / (float)D;
   float4 v[RPW][NCH];
   float s[RPW];
 #pragma unroll
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
   for (int q = 0; q < RPW; q++) {
     const int row = row0 + q;
     if (row >= rows) break;
-    const float mean = wave_sum(s[q]) / D;
+    const float mean = wave_sum(s[q]) * invd;
     float qq = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
         qq += (a * a + bb * bb) + (cc * cc + d * d);
       }
     }
-    const float inv = rsqrtf(wave_sum(qq) / D + eps);
+    const float inv = rsqrtf(fmaf(wave_sum(qq), invd, eps));
     const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
     float4 ov[MR ? NCH : 1];
 #pragma unroll
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
 #pragma unroll
       for (int j = 0; j < NCH; j++)
         if (lane + 64 * j < nc) os += (ov[j].x + ov[j].y) + (ov[j].z + ov[j].w);
-      const float om = wave_sum(os) / D;
+      const float om = wave_sum(os) * invd;
       float oq = 0.f;
 #pragma unroll
       for (int j = 0; j < NCH; j++)
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
           const float a = ov[j].x - om, bb = ov[j].y - om, cc = ov[j].z - om, d = ov[j].w - om;
           oq += (a * a + bb * bb) + (cc * cc + d * d);
         }
-      const float orr = rsqrtf(wave_sum(oq) / D + eps);
+      const float orr = rsqrtf(fmaf(wave_sum(oq), invd, eps));
       if (lane == 0) reinterpret_cast<float2*>(ymr)[row] = make_float2(om, orr);
     }
   }
