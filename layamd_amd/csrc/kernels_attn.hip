@@ -504,9 +504,11 @@ void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt
                       const AttnTile* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
                       const int* gq, const int* grow, int window_half, float scale, hipStream_t st) {
   if (ntiles <= 0) return;
-  if (qtile != 64 && !(qtile == 128 && sizeof(T) == 2 && !gq)) {
-    fprintf(stderr, "[laya] attention: unsupported query tile %d\n", qtile);
-    abort();
+  // (128-query tiles give the 64-query tiles' bits only when a sliding window's half width is a
+  // multiple of the 64-key block: then both tilings start their key blocks at the same keys)
+  if (qtile != 64 && !(qtile == 128 && sizeof(T) == 2 && !gq && window_half % 64 == 0)) {
+    fprintf(stderr, "[laya] attention: unsupported query tile %d (window half %d)\n", qtile, window_half);
+    exit(1);
   }
   if constexpr (sizeof(T) == 2) {
     if (qtile == 128)
