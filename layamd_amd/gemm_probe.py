@@ -14,6 +14,11 @@ times the GEMM microbenchmark shapes instead: M in {512, 16384}, (N, K) in {(307
 rocBLAS) on the same device.  bf16 tries the planner and every tile configuration (with split-K
 factors 2, 4 and 8 at M = 512 where K allows them) and reports the best; each engine result is checked
 against torch.mm.  Prints a markdown table.
+
+    python -m layamd_amd.gemm_probe --c3
+
+does the same, bf16 only, for the encoder GEMMs of the b32 x s512 ModernBERT-large pass: M = 9664
+rows (the pass's 9514 tokens, packed and padded to 64), (N, K) as above.
 """
 import argparse
 import time
@@ -21,7 +26,9 @@ import time
 from layamd_amd import engine as le
 
 
-C2_SHAPES = [(M, N, K) for M in (512, 16384) for (N, K) in ((3072, 1024), (1024, 1024), (5248, 1024), (1024, 2624))]
+ENCODER_NK = ((3072, 1024), (1024, 1024), (5248, 1024), (1024, 2624))
+C2_SHAPES = [(M, N, K) for M in (512, 16384) for (N, K) in ENCODER_NK]
+C3_SHAPES = [(9664, N, K) for (N, K) in ENCODER_NK]
 
 
 def _spin():
@@ -46,17 +53,18 @@ def _time(fn, iters=20):
     return a.elapsed_time(b) / iters * 1e3                # us per call
 
 
-def c2(lib):
+def c2(lib, shapes=C2_SHAPES, dtypes=None):
     import torch
+    dtypes = dtypes or (torch.bfloat16, torch.float32)
     g = torch.Generator(device="cpu").manual_seed(0)
     ws = torch.empty(64 << 20, dtype=torch.float32, device="cuda")   # split-K partials (256 MiB)
     print("| M | N | K | dtype | torch.mm us | TFLOP/s | engine us | TFLOP/s | engine plan | planner us | max rel err vs torch.mm |")
     print("|---:|---:|---:|---|---:|---:|---:|---:|---|---:|---:|")
-    for (M, N, K) in C2_SHAPES:
+    for (M, N, K) in shapes:
         fl = 2.0 * M * N * K
         A32 = torch.randn(M, K, generator=g).cuda()
         W32 = (torch.randn(N, K, generator=g) * 0.02).cuda()
-        for dt in (torch.bfloat16, torch.float32):
+        for dt in dtypes:
             A, W = A32.to(dt), W32.to(dt)
             Wt = W.t()
             ref = torch.empty(M, N, dtype=dt, device="cuda")
@@ -96,6 +104,7 @@ def main():
     ap.add_argument("--cfg", type=int, default=0)
     ap.add_argument("--iters", type=int, default=4)
     ap.add_argument("--c2", action="store_true", help="time the microbenchmark shapes against torch.mm")
+    ap.add_argument("--c3", action="store_true", help="time the b32 x s512 pass's encoder GEMM shapes against torch.mm")
     ap.add_argument("--torch", action="store_true",
                     help="after the engine launches, run torch.mm on the same operands as many times")
     a = ap.parse_args()
@@ -103,6 +112,9 @@ def main():
     import torch
     if a.c2:
         c2(lib)
+        return
+    if a.c3:
+        c2(lib, C3_SHAPES, (torch.bfloat16,))
         return
     g = torch.Generator(device="cpu").manual_seed(0)
     A = torch.randn(a.M, a.K, generator=g).to(torch.bfloat16).cuda()
