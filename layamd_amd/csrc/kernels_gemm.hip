@@ -373,6 +373,12 @@ __device__ __forceinline__ uint32_t dma64_voff(int row0, int r8, int ld_bytes, i
   return (uint32_t)(row0 + r8 + rl) * (uint32_t)ld_bytes + ((uint32_t)((lane & 7) ^ rl ^ odd) << 4);
 }
 
+// RoPE table rows in LDS (128 bytes: 32 floats, of cos or of sin): 16-byte chunk c of row r sits in
+// slot c ^ rope_sw(r).  The epilogue's reads (lanes on 16 consecutive rows, one chunk each) then
+// cover 16 distinct 16-byte bank positions; unswizzled, the 128-byte row stride put eight of them
+// on the same banks.
+__device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
+
 // DMA plan of one workgroup for 64-deep stages: PA + PB instructions per wave and stage.  The
 // per-lane offset depends only on the parity of the instruction index (the swizzle's row term);
 // the instruction's row step and the stage's K offset go in the scalar offset.
@@ -763,10 +769,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       // All offsets first, each pinned by an empty statement that uses it: the compiler's waits for
       // the position loads (which in hardware also wait for every fill issued after them) then
       // come together here, not between table fills, where each would wait for the fills before it.
+      // (LDS slot lane % 8 of table row r holds the row's 16-byte chunk (lane % 8) ^ rope_sw(r))
       uint32_t voff[NT];
 #pragma unroll
       for (int k = 0; k < NT; k++) {
-        voff[k] = (uint32_t)pp[k] * 128u + (uint32_t)(lane & 7) * 16u;
+        voff[k] = (uint32_t)pp[k] * 128u + (uint32_t)((lane & 7) ^ rope_sw((tid + 256 * k) >> 3)) * 16u;
         asm volatile("" ::"v"(voff[k]));
       }
 #pragma unroll
@@ -856,8 +863,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_wave_barrier();
   };
-  // byte offset of 16-byte chunk q of staged row r (cpr chunks per row, a power of two)
-  auto sidx = [](int r, int q, int cpr) { return (r * cpr + (q ^ (r & (cpr - 1)))) * 16; };
+  // byte offset of 16-byte chunk q of staged row r (cpr chunks per row, a power of two).  The chunk
+  // is XORed with the row's index among the rows that share one pass over the 64 banks (256 bytes:
+  // 16 / cpr rows for short rows), so that the 32 rows a column of lanes writes at once spread over
+  // every chunk position of their bank range (8-byte writes: 2-way at most; 16-byte: none), while a
+  // flush pass, 16 lanes over whole rows that share that index, stays conflict-free.
+  auto sidx = [](int r, int q, int cpr) {
+    const unsigned rpl = cpr >= 16 ? 1u : 16u / (unsigned)cpr;
+    return (r * cpr + (q ^ (int)(((unsigned)r / rpl) & (unsigned)(cpr - 1)))) * 16;
+  };
   // four bf16 values at staged row r, columns c..c+3 (c % 4 == 0)
   auto put8 = [&](int r, int c, int cpr, float v0, float v1, float v2, float v3) {
     uint2 u;
@@ -1081,8 +1095,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           for (int k = 0; k < NB; k++) {
             if (k0 + k >= NT) break;
             const int it = tid + 256 * (k0 + k), r = it >> 3, q = it & 7;
-            *reinterpret_cast<float4*>(tcos + r * 32 + 4 * q) = tc[k];
-            *reinterpret_cast<float4*>(tsin + r * 32 + 4 * q) = ts[k];
+            *reinterpret_cast<float4*>(tcos + r * 32 + 4 * (q ^ rope_sw(r))) = tc[k];
+            *reinterpret_cast<float4*>(tsin + r * 32 + 4 * (q ^ rope_sw(r))) = ts[k];
           }
         }
       }
@@ -1110,8 +1124,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
               float o1[4], o2[4];
               if (rope) {
                 // rotate_half partners (d, d + 32) of a head are blocks jp, jp + 1 of one lane
-                const f32x4_t cs = *reinterpret_cast<const f32x4_t*>(tcos + r * 32 + dd);
-                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(tsin + r * 32 + dd);
+                const int tq = r * 32 + 4 * ((dd >> 2) ^ rope_sw(r));
+                const f32x4_t cs = *reinterpret_cast<const f32x4_t*>(tcos + tq);
+                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(tsin + tq);
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                   // explicit fused forms: left to contraction, different tile shapes could round
