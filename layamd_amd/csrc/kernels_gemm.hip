@@ -33,6 +33,7 @@
 #include "kernels.h"
 
 #include <atomic>
+#include <type_traits>
 
 namespace laya {
 
@@ -398,6 +399,15 @@ struct XlDma64 {
   }
 };
 
+// f(integral_constant<int, I>) for I = B .. E - 1, in order
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // fragment idx (A blocks, then W blocks) of 16-deep sub-step s of a 64-deep stage
 template <int FM, int FN>
 __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32x4_t* As, const u32x4_t* Bs, int arow,
@@ -419,9 +429,14 @@ __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32
 // over three sub-steps leaves the last part too little time to land before the wait.  Every stage
 // but the last issues the same DMA instructions (past the last stage they read nothing), so the
 // wait is a constant vmcnt(0).  K is a multiple of 64 (every stage is whole).
-template <bool SWAP, int NX, int FM, int FN, int PA, int PB, class ST>
+// XP > 0: the first XP stages each also issue piece p of the caller's loads (xl(p), XS vector-memory
+// instructions, e.g. the residual GEMM's x), after the W part of their next stage.  Their wait then
+// leaves those XS loads in flight, vmcnt(XS), and the next stage's wait covers them, so each piece
+// has about a stage and a half to land while the MFMAs run.  Pieces of stages that K does not
+// reach are issued after the loop.
+template <bool SWAP, int NX, int XP, int XS, int FM, int FN, int PA, int PB, class ST, class XL>
 __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST& T1, const XlDma64<PA, PB>& d, int arow,
-                                            int brow, int hi, int sw) {
+                                            int brow, int hi, int sw, XL&& xl) {
   constexpr int NMM = FM * FN, E = FM + FN, EW = PB + FM + FN, EA = PA + FM + FN;
   Frags<FM, FN> F0, F1;
   // stage 0; the A part of stage 1 and NX later fills the caller issued may still be in flight
@@ -440,8 +455,9 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
   }
   // stage g in buffer C, followed by stage g + 1 in buffer N.  The first sub-step also issues the W
   // part of stage g + 1 (into N, free since the previous stage's barrier) and the fourth the A
-  // part of stage g + 2, so a stage's fills leave in two bursts half the size of one.
-#define LAYA_STAGE64(C, N)                                                                \
+  // part of stage g + 2, so a stage's fills leave in two bursts half the size of one.  P >= 0:
+  // piece P of the caller's loads follows the W part.
+#define LAYA_STAGE64(C, N, P)                                                             \
   {                                                                                       \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
       mma_one_x<SWAP>(acc, F0, t);                                                        \
@@ -451,9 +467,14 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
       }                                                                                   \
       __builtin_amdgcn_sched_barrier(0);                                                  \
     }                                                                                     \
+    if constexpr (P >= 0) {                                                               \
+      xl(std::integral_constant<int, P>{});                                               \
+      __builtin_amdgcn_sched_barrier(0);                                                  \
+    }                                                                                     \
     LAYA_SUB64(F1, F0, C, 2)                                                              \
     LAYA_SUB64(F0, F1, C, 3)                                                              \
-    LAYA_WAIT_VMCNT(0);                                                                   \
+    if constexpr (P >= 0) LAYA_WAIT_VMCNT(XS);                                            \
+    else LAYA_WAIT_VMCNT(0);                                                              \
     __builtin_amdgcn_s_barrier();                                                         \
     asm volatile("" ::: "memory");                                                        \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
@@ -468,11 +489,22 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
   }
   const int nst = d.ns / 2;                // stages
   int g = 0;
-  for (; g + 2 < nst;) {                   // two stages, each followed by another
-    LAYA_STAGE64(T0, T1)
-    LAYA_STAGE64(T1, T0)
+  int xdone = 0;                           // pieces issued
+  if constexpr (XP > 0) {
+    static_for<0, (XP + 1) / 2>([&](auto q) {  // the stages that carry pieces, two at a time
+      constexpr int P0 = 2 * decltype(q)::value, P1 = P0 + 1 < XP ? P0 + 1 : -1;
+      if (g + 2 < nst) {
+        LAYA_STAGE64(T0, T1, P0)
+        LAYA_STAGE64(T1, T0, P1)
+        xdone = P1 < 0 ? XP : P1 + 1;
+      }
+    });
   }
-  if (g + 2 == nst) LAYA_STAGE64(T0, T1)   // g is even: stage g in T0; the last one is in T1
+  for (; g + 2 < nst;) {                   // two stages, each followed by another
+    LAYA_STAGE64(T0, T1, -1)
+    LAYA_STAGE64(T1, T0, -1)
+  }
+  if (g + 2 == nst) LAYA_STAGE64(T0, T1, -1)  // g is even: stage g in T0; the last one is in T1
   ST& L = (g & 1) ? T1 : T0;               // the last stage (g == nst - 1)
   LAYA_SUB64(F0, F1, L, 1)
   LAYA_SUB64(F1, F0, L, 2)
@@ -482,6 +514,11 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
 #undef LAYA_STAGE64
 #undef LAYA_SUB64
   LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
+  if constexpr (XP > 0) {
+    static_for<0, XP>([&](auto p) {        // pieces of stages K did not reach
+      if (decltype(p)::value >= xdone) xl(p);
+    });
+  }
 }
 
 
@@ -802,38 +839,58 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // e % 4 (four consecutive rows per e / 4) and column cbase + 32 j + lane % 32.
   const int rbase = m0 + wm * WTM, cbase = n0 + wn * WTN;
   f32x16_t acc[FM][FN];
-  if constexpr (EPI == EPI_RESID) {
-    // the residual update X += A W^T + b starts the accumulators at X (16-byte loads of 4 columns;
-    // rows past M read 0, columns past N are never stored), so the epilogue loads nothing after its
-    // first store.  These loads come after the DMA fills, so the wait for them (before the K loop)
-    // also covers the prologue stages.
-    const __amdgpu_buffer_rsrc_t rX =
-        __builtin_amdgcn_make_buffer_rsrc(a.X, (short)0, (int)((size_t)a.M * a.ldx * sizeof(float)), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+  // The residual update X += A W^T + b adds X to the finished product, (A W^T + X) + b, in the
+  // accumulator layout: block (i, j) of the lane's X is four 16-byte loads of 4 columns (rows past
+  // M read 0, columns past N are never stored).  Where does X wait in registers?
+  //   XIN: tiles alone on their CU with the two-buffer loop and room for a second register copy of
+  //        the accumulators: the K loop's first FM FN stages each issue one block (the HBM reads
+  //        spread over the loop instead of holding up its first stage);
+  //   XPRE: other tiles with room for the copy: all of it before the K loop, one wait;
+  //   otherwise (XEPI) the epilogue loads each block row as it comes to it, or, for tiles alone
+  //        on their CU, a block row ahead (two workgroups on a CU cover each other's waits).
+  // The sum and its order are the same in all three.
+  constexpr bool XRES = EPI == EPI_RESID;
+  constexpr bool ONE_PER_CU = NST * 16 > 80 * 1024;
+  constexpr bool XIN = XRES && LOOP == 0 && ONE_PER_CU && FM * FN * 16 <= 160;
+  constexpr bool XPRE = XRES && !XIN && FM * FN * 16 <= 64;
+  constexpr bool XEPI = XRES && !XIN && !XPRE;
+  f32x4_t xr[XIN || XPRE ? FM : 1][XIN || XPRE ? FN : 1][4];
+  const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
+      XRES ? a.X : nullptr, (short)0, XRES ? (int)((size_t)a.M * a.ldx * sizeof(float)) : 0, 0x00020000);
+  // X at rows rbase + 32 i + lane % 32, columns cbase + 32 j + 8 g + 4 hi .. + 3
+  auto xload = [&](int i, int j, int g) -> f32x4_t {
+    const uint32_t off = ((uint32_t)(rbase + i * 32 + l32) * (uint32_t)a.ldx + (uint32_t)(cbase + j * 32 + 8 * g + 4 * hi)) * 4u;
+    // reinterpret the whole 16 bytes as floats (a bit_cast of one vector component is miscompiled
+    // by this compiler: it reads component 0)
+    return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
+  };
+  // piece p of XIN: block (p / FN, p % FN)
+  auto xpiece = [&](auto p) {
+    if constexpr (XIN) {
+      constexpr int i = decltype(p)::value / FN, j = decltype(p)::value % FN;
+#pragma unroll
+      for (int g = 0; g < 4; g++) xr[i][j][g] = xload(i, j, g);
+    }
+  };
+  if constexpr (XPRE) {
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int j = 0; j < FN; j++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const uint32_t off = ((uint32_t)(rbase + i * 32 + l32) * (uint32_t)a.ldx + (uint32_t)(cbase + j * 32 + 8 * g + 4 * hi)) * 4u;
-          // reinterpret the whole 16 bytes as floats (a bit_cast of one vector component is
-          // miscompiled by this compiler: it reads component 0)
-          const f32x4_t x = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
-#pragma unroll
-          for (int u = 0; u < 4; u++) acc[i][j][4 * g + u] = x[u];
-        }
+        for (int g = 0; g < 4; g++) xr[i][j][g] = xload(i, j, g);
     // Wait for these loads once, here, with a wait the compiler sees (not inline assembly).  Left to
-    // itself it places the waits at the MFMAs inside the K loop and, since its wait analysis merges
-    // the loop entry into every iteration, repeats them there: vmcnt(44..0) at the top of each
-    // iteration, which after the first one wait for the next stage's DMA fills instead.
+    // itself it would wait where the epilogue reads them, and its wait analysis, which merges the
+    // loop entry into every iteration, could repeat such waits inside the K loop, where they would
+    // wait for the next stage's DMA fills instead.  These loads come after the prologue fills, so
+    // this wait covers those too.
     __builtin_amdgcn_s_waitcnt(0x0F70);                   // vmcnt(0); expcnt, lgkmcnt: no wait
-  } else {
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
   }
 
   const int arow = wm * WTM + l32, brow = wn * WTN + l32;
@@ -846,8 +903,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     if (swap) xl_k_loop64d<true, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
     else xl_k_loop64d<false, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
   } else {
-    if (swap) xl_k_loop64<true, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
-    else xl_k_loop64<false, NTX>(acc, T0, T1, dm, arow, brow, hi, sw);
+    if constexpr (XIN) {
+      if (swap) xl_k_loop64<true, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece);
+      else xl_k_loop64<false, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece);
+    } else {
+      auto none = [](auto) {};
+      if (swap) xl_k_loop64<true, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none);
+      else xl_k_loop64<false, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none);
+    }
   }
 
   // ---------------- epilogue ----------------
@@ -855,8 +918,9 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // writes the block (bias, activation, GeGLU, RoPE applied in registers) into its quarter of the
   // staging area as rows of 16-byte chunks, swizzled by row, then streams whole rows out with
   // 16-byte stores (full cache lines).  The K stages hold the RoPE tables for the QKV projection.
-  // All global loads are issued before the first store: on gfx9 vmcnt counts stores too, so a load
-  // issued after a store would wait for it.
+  // Global loads are issued before the first store (on gfx9 vmcnt counts stores too, so a load
+  // issued after a store would wait for it), except the XEPI residual loads, each issued a block
+  // row ahead of its use.
   __syncthreads();                                        // every wave is done with the K stages
   char* stg = reinterpret_cast<char*>(L) + wave * SB;
   auto sync_wave = [] {                                   // this wave's LDS writes are visible to it
@@ -954,8 +1018,38 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     // (lower half first) by Chan et al.'s pairwise update, M2 = M2a + M2b + (Sb - Sa)^2 nb / (na n).
     // The values, their order and the arithmetic do not depend on the tile shape.
     float ls0 = 0.f, lq0 = 0.f;                           // the lane's first block of a group
+    // XEPI: X of block row i (and i + 1 with XAHEAD), in xb[i % XB]
+    constexpr bool XAHEAD = XEPI && ONE_PER_CU;
+    constexpr int XB = XAHEAD ? 2 : 1;
+    f32x4_t xb[XB][XEPI ? FN : 1][4];
+    if constexpr (XAHEAD) {
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) xb[0][j][g] = xload(0, j, g);
+    }
+    // acc + X of block (i, j), elements 4 g .. 4 g + 3
+    auto accx = [&](int i, int j, int g) -> f32x4_t {
+      f32x4_t v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+      if constexpr (XRES) {
+        f32x4_t x;
+        if constexpr (XEPI) x = xb[i % XB][j][g];
+        else x = xr[i][j][g];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = __fadd_rn(v[u], x[u]);
+      }
+      return v;
+    };
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      if constexpr (XEPI) {
+        const int il = XAHEAD ? i + 1 : i;                // the block row to load
+        if (il < FM)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) xb[il % XB][j][g] = xload(il, j, g);
+      }
 #pragma unroll
       for (int cp = 0; cp < WTN / CW; cp++) {
 #pragma unroll
@@ -963,11 +1057,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           float v16[16];
 #pragma unroll
           for (int g = 0; g < 4; g++) {
+            const f32x4_t s4 = accx(i, j, g);
             float4 v;
-            v.x = ab(acc[i][j][4 * g + 0], bb[j][g].x);
-            v.y = ab(acc[i][j][4 * g + 1], bb[j][g].y);
-            v.z = ab(acc[i][j][4 * g + 2], bb[j][g].z);
-            v.w = ab(acc[i][j][4 * g + 3], bb[j][g].w);
+            v.x = ab(s4[0], bb[j][g].x);
+            v.y = ab(s4[1], bb[j][g].y);
+            v.z = ab(s4[2], bb[j][g].z);
+            v.w = ab(s4[3], bb[j][g].w);
             *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
             v16[4 * g + 0] = v.x; v16[4 * g + 1] = v.y; v16[4 * g + 2] = v.z; v16[4 * g + 3] = v.w;
           }
@@ -1010,16 +1105,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 #pragma unroll
           for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPH, ab(acc[i][j][4 * g + 0], bb[j][g].x),
-                   ab(acc[i][j][4 * g + 1], bb[j][g].y), ab(acc[i][j][4 * g + 2], bb[j][g].z),
-                   ab(acc[i][j][4 * g + 3], bb[j][g].w));
+            for (int g = 0; g < 4; g++) {
+              const f32x4_t s4 = accx(i, j, g);
+              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPH, ab(s4[0], bb[j][g].x), ab(s4[1], bb[j][g].y),
+                   ab(s4[2], bb[j][g].z), ab(s4[3], bb[j][g].w));
+            }
           flush(CPH, [&](int r) -> char* {
             const int m = rbase + i * 32 + r;
             return m < a.M ? reinterpret_cast<char*>(a.Xh + (size_t)m * a.ldxh + c0) : nullptr;
           }, nchunks(a.N - c0, 8, CPH));
         }
       }
+    }
   } else if constexpr (EPI == EPI_STORE || EPI == EPI_GEGLU) {
     // bf16 rows of OW output columns, blocks of 32 rows x CW columns
     constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;
