@@ -62,6 +62,14 @@ int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, con
  * achievable peak next to the published one.  Returns 0, or -1 for invalid arguments. */
 int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* flops);
 
+/* The chip's achievable HBM rate: launches (does not wait for) a copy of bytes from src to dst on
+ * stream, non-temporal 16-byte loads and stores from two workgroups per CU striding over the range.
+ * The caller times it with its own events (bytes read + bytes written per second).  No counterpart
+ * in the reference: it gives bench.py a hand-written copy as the achievable bandwidth next to the
+ * published one.  Returns 0, or -1 when bytes is 0 or not a multiple of 16, a pointer is null or
+ * not 16-byte aligned, or the ranges overlap. */
+int laya_ext_hbm_copy(const void* src, void* dst, size_t bytes, void* stream);
+
 /* Pins the bf16 GEMM tile configuration of every later launch, process-wide: -1 removes the pin
  * (each engine's plans, or its own LAYA_GEMM_CFG read at laya_create, apply); 0..8 select 256x256, 256x128, 128x256, 128x128,
  * 192x256, 160x256, 128x192, 192x128 or 128x64 tiles (the QKV projection falls back to a shape that keeps its tiles inside one of

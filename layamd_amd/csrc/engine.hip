@@ -951,6 +951,24 @@ int laya_ext_mfma_loop(float* out, int blocks, int iters, void* stream, double* 
   return 0;
 }
 
+// launch only, like the MFMA loop: two workgroups per CU
+int laya_ext_hbm_copy(const void* src, void* dst, size_t bytes, void* stream) {
+  using namespace laya;
+  if (!src || !dst || bytes == 0 || bytes % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+    return -1;
+  const char* s = static_cast<const char*>(src);
+  const char* d = static_cast<const char*>(dst);
+  if (s < d + bytes && d < s + bytes) return -1;         // overlapping ranges
+  (void)hipGetLastError();
+  int dev = 0, cus = 0;
+  LAYA_HIP(hipGetDevice(&dev));
+  LAYA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  launch_hbm_copy(src, dst, bytes / 16, 2 * (cus > 0 ? cus : 256), (hipStream_t)stream);
+  LAYA_HIP(hipGetLastError());
+  return 0;
+}
+
 int laya_ext_gemm(int dtype, int epi, const void* A, const void* W, void* C, const float* bias, int act, int M, int N,
                   int K, void* stream, int iters, float* ms) {
   using namespace laya;

@@ -95,6 +95,8 @@ constexpr int kGemmConfigs = 9;
 // the achievable-MFMA probe: blocks x 4 waves, each iters x 8 MFMAs of 32x32x16 bf16 (32768 flop);
 // out holds blocks x 256 floats
 void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st);
+// device copy of n16 16-byte chunks (16-byte aligned), non-temporal, on blocks workgroups
+void launch_hbm_copy(const void* src, void* dst, size_t n16, int blocks, hipStream_t st);
 // whether a bf16 launch of this shape can run tile configuration cfg (false for every cfg when the
 // shape needs the generic kernel); the analytic planner's pick for it (-1: generic kernel)
 bool gemm_config_valid(int epi, const GemmArgs& a, int cfg);

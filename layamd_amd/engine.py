@@ -26,7 +26,7 @@ ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act"
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
                "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop",
-               "laya_ext_stats", "laya_ext_attention", "laya_ext_gemm_splitk_static"]
+               "laya_ext_stats", "laya_ext_attention", "laya_ext_gemm_splitk_static", "laya_ext_hbm_copy"]
 # every environment variable laya_create reads; Engine() sets the ones it is given for the duration
 # of laya_create only
 ENV_KNOBS = ["LAYA_PRECISION", "LAYA_MAX_TOKENS", "LAYA_PASS_TOKENS", "LAYA_MAX_SEQS", "LAYA_MAX_GATHERED",
@@ -93,6 +93,8 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.POINTER(ctypes.c_double)]
     L.laya_ext_mfma_loop.restype = ctypes.c_int
+    L.laya_ext_hbm_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.laya_ext_hbm_copy.restype = ctypes.c_int
     L.laya_ext_stats.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_longlong), ctypes.c_int]
     L.laya_ext_stats.restype = ctypes.c_int
     L.laya_ext_attention.argtypes = ([ctypes.c_int] + [ctypes.c_void_p] * 2 + [ctypes.c_int] * 2 + [ctypes.c_void_p, ctypes.c_int,
@@ -154,6 +156,34 @@ def mfma_peak(lib, blocks_per_cu: int = 2, iters: int = 4096) -> float:
     b.record()
     torch.cuda.synchronize()
     return flops.value / (a.elapsed_time(b) * 1e-3) / 1e12
+
+
+def hbm_copy(lib, src, dst) -> None:
+    """Launches the library's HBM copy of torch device tensor src into dst (same byte size, on the
+    current stream); raises ValueError when the library rejects it."""
+    import torch
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("hbm_copy: sizes differ")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if lib.laya_ext_hbm_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes, st) != 0:
+        raise ValueError("hbm_copy rejected")
+
+
+def hbm_peak(lib, nbytes: int = 1 << 30, iters: int = 5) -> float:
+    """The chip's achievable HBM rate in GB/s: bytes read plus bytes written per second by the
+    library's stream copy over two buffers of nbytes, iters launches back to back."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    hbm_copy(lib, src, dst)                                # warm-up
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        hbm_copy(lib, src, dst)
+    b.record()
+    torch.cuda.synchronize()
+    return 2.0 * nbytes * iters / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
 def gemm_ksplit(lib, ks: int, ws=None) -> int:

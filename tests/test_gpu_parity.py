@@ -188,6 +188,49 @@ def test_fp32_gemm_rows_independent_of_tiling(part):
     assert torch.equal(X1[:part].cpu(), X2.cpu())
 
 
+@pytest.mark.parametrize("nbytes", [16, 16 * 1023, 16 * 1025, (1 << 20) + 48, 3 << 24])
+def test_hbm_copy_probe_copies(nbytes):
+    """The achievable-bandwidth copy moves every byte: sizes that leave a partial round of 1024
+    chunks per workgroup, or fewer chunks than threads, come back bit for bit, and the bytes next
+    to the destination range stay untouched."""
+    import torch
+    lib = le.load_library()
+    g = torch.Generator(device="cpu").manual_seed(nbytes % 1000)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g).cuda()
+    dst = torch.full((nbytes + 64,), 7, dtype=torch.uint8, device="cuda")
+    le.hbm_copy(lib, src, dst[:nbytes])
+    torch.cuda.synchronize()
+    out = dst.cpu()
+    assert torch.equal(out[:nbytes], src.cpu())
+    assert bool((out[nbytes:] == 7).all())
+
+
+def test_hbm_copy_probe_rejects():
+    """Sizes that are not whole 16-byte chunks, misaligned or overlapping ranges are refused
+    before anything is launched."""
+    import ctypes
+    import torch
+    lib = le.load_library()
+    buf = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    p = buf.data_ptr()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    f = lib.laya_ext_hbm_copy
+    assert f(ctypes.c_void_p(p), ctypes.c_void_p(p + 2048), 40, st) == -1       # not a multiple of 16
+    assert f(ctypes.c_void_p(p + 8), ctypes.c_void_p(p + 2048), 64, st) == -1   # misaligned source
+    assert f(ctypes.c_void_p(p), ctypes.c_void_p(p + 1024), 2048, st) == -1     # overlapping
+    assert f(ctypes.c_void_p(p), ctypes.c_void_p(p + 2048), 0, st) == -1
+    assert f(None, ctypes.c_void_p(p), 64, st) == -1
+    assert f(ctypes.c_void_p(p), ctypes.c_void_p(p + 2048), 2048, st) == 0
+    torch.cuda.synchronize()
+
+
+def test_hbm_copy_probe_rate():
+    """The copy reports a rate between a tenth of the published 8 TB/s and the peak itself."""
+    lib = le.load_library()
+    gbs = le.hbm_peak(lib, 256 << 20, 3)
+    assert 800.0 < gbs < 8000.0, gbs
+
+
 def test_mfma_loop_probe():
     """The achievable-peak probe runs and reports a rate between a tenth of the published bf16
     peak and the peak itself (the chip cannot beat 2.5166 PF; a broken probe reads far lower)."""
