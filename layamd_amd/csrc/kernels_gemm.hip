@@ -22,7 +22,8 @@
 //
 // Epilogues:
 //   EPI_STORE  C = act(acc + bias)                        (storage type)
-//   EPI_RESID  X += acc + bias                            (fp32 residual stream)
+//   EPI_RESID  X += acc + bias (fp32 residual stream), rounded as X + (acc + bias) in k_gemm and as
+//              (acc + X) + bias in k_gemm_xl
 //   EPI_QKV    q,k (RoPE when tables are given) -> Q, K [rows][H*HD]; v -> V^T [H*HD][ldv] at
 //              column = row.  A wave's column range covers whole 64-wide heads, so the
 //              rotate_half partners (d, d+32) of a row sit in the same lane.
