@@ -12,9 +12,13 @@ pass's few-KB index arrays are re-copied from pinned memory), bracketed by
 torch.cuda.synchronize().  `abi_seqs_per_s` times the same K steps through laya_forward_batch
 (host packing, H2D/D2H and synchronisation included).
 
-roofline: per-stage device times come from HIP events on the engine's stream
-(laya_ext_prof_enable); the dominant kernel's achieved rate is its algorithmic work per launch
-(2*M*N*K flops for a GEMM over the valid tokens) divided by its average launch time.
+roofline: per-stage device times are kernel times: with laya_ext_prof_enable every kernel of a
+profiled pass records its own start and end (hipExtLaunchKernel events on the engine's stream,
+nothing waiting between launches), summed per stage; the dominant kernel's achieved rate is its
+algorithmic work per launch (2*M*N*K flops for a GEMM over the valid tokens) divided by its
+average launch time.  `traffic` is the dominant kernel's HBM traffic per launch from the
+committed rocprofv3 --pmc summary, reported only when that summary was measured on the GEMM
+sources being benched (their hash is recorded beside the figure).
 
 cpu_baseline: the CPU PyTorch restatement of the reference path (oracle/model.py, fp32 torch on
 this host's cores): the first questions of the same batch (about cpu-budget seconds), plus the
@@ -40,19 +44,41 @@ PMC_COPY_BYTES = 256 << 20
 # calibrated HBM traffic per launch of the dominant kernel, from the committed rocprofv3 --pmc
 # summary (FETCH_SIZE and WRITE_SIZE runs of `bench.py --pmc-probe`, scaled by the copy kernel)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "c3_geglu_gemm_hbm_traffic.md")
-TRAFFIC_SOURCE = ("recorded, not measured in this run: profiles/c3_geglu_gemm_hbm_traffic.md (rocprofv3 --pmc "
-                  "FETCH_SIZE and WRITE_SIZE runs of bench.py --pmc-probe, copy-calibrated)")
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of bench.py --pmc-probe, copy-calibrated, "
+                  "recorded in profiles/c3_geglu_gemm_hbm_traffic.md for GEMM sources with hash %s (the sources "
+                  "benched here)")
+# the sources that decide the GEMM kernel's memory traffic
+GEMM_SOURCES = [os.path.join(REPO, "layamd_amd", "csrc", f) for f in ("kernels_gemm.hip", "kernels.h", "common.h")]
+
+
+def gemm_source_hash():
+    import hashlib
+    h = hashlib.sha256()
+    for f in GEMM_SOURCES:
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(kernel_stage):
-    """Bytes per launch recorded for kernel_stage in the traffic summary, or None."""
+    """(bytes per launch, source note) recorded for kernel_stage in the traffic summary when it was
+    measured on the GEMM sources of this tree, else (None, why)."""
+    rec, src = None, None
     try:
         for line in open(TRAFFIC_FILE):
             if line.startswith("traffic_bytes_per_launch ") and line.split()[1] == kernel_stage:
-                return int(line.split()[2])
+                rec = int(line.split()[2])
+            if line.startswith("gemm_sources_sha256_16 "):
+                src = line.split()[1]
     except OSError:
-        pass
-    return None
+        return None, "no traffic summary"
+    if rec is None:
+        return None, "no traffic recorded for %s" % kernel_stage
+    here = gemm_source_hash()
+    if src != here:
+        return None, ("the recorded traffic (%d bytes) was measured on GEMM sources %s, not these (%s): dropped"
+                      % (rec, src, here))
+    return rec, TRAFFIC_SOURCE % here
 
 
 def stage_work(name, cfg, T, R, KT, B, elt, attn_flops):
@@ -232,7 +258,7 @@ def main():
           % (a.config, ms_per_step, dev_ms / a.steps, seqs_s, tok_s, 1000 * abi_wall / a.steps),
           file=sys.stderr, flush=True)
 
-    # per-stage device times (event-bracketed, graphs bypassed)
+    # per-stage kernel times (each kernel's own start and end events, graphs bypassed)
     eng.prof_enable(True)
     eng.prof_reset()
     n_prof = 3
@@ -299,15 +325,17 @@ def main():
     if fl and "gemm" in dom:
         ach = fl / (dom_ms * 1e-3) / 1e12
         peak = (PEAK_BF16 if elt == 2 else PEAK_FP32) / 1e12
+        traffic, tsrc = measured_traffic(dom)
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4), "traffic": measured_traffic(dom), "traffic_source": TRAFFIC_SOURCE,
+                "frac": round(ach / peak, 4), "traffic": traffic, "traffic_source": tsrc,
                 "kernel": dom,
                 "work_per_launch": "2*T*N*K = %.4g flop (T=%d valid tokens)" % (fl, T),
                 "achievable_peak": round(mfma_ach, 1), "frac_of_achievable": round(ach / mfma_ach, 4)}
     else:
         ach = by / (dom_ms * 1e-3) / 1e9
+        traffic, tsrc = measured_traffic(dom)
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": measured_traffic(dom), "traffic_source": TRAFFIC_SOURCE,
+                "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": traffic, "traffic_source": tsrc,
                 "kernel": dom,
                 "achievable_peak": round(copy_gbs, 1), "frac_of_achievable": round(ach / copy_gbs, 4)}
 

@@ -8,9 +8,11 @@
 extern "C" {
 #endif
 
-/* Turns per-stage event timing on (1) or off (0) at run time.  While on, every stage is bracketed
- * by HIP events on the engine's stream and synchronised, and HIP graphs are bypassed.  Returns the
- * previous state. */
+/* Turns per-stage kernel timing on (1) or off (0) at run time.  While on, HIP graphs are bypassed
+ * and every kernel a stage launches records its own device start and end time in a pair of HIP
+ * events (hipExtLaunchKernel), with no marker or synchronisation between launches; a stage's time
+ * is the sum of its kernels' durations, read once the pass has finished.  Returns the previous
+ * state. */
 int laya_ext_prof_enable(void* h, int on);
 
 /* Stage i of the profile table: copies its name (NUL-terminated, at most name_len bytes), total

@@ -2,6 +2,7 @@
 // (bf16 storage with fp32 math, or fp32), and wave64 reductions.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -10,6 +11,27 @@
   fprintf(stderr, "[laya] HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); exit(1); } } while (0)
 
 namespace laya {
+
+// Kernel timing for the stage profiler.  While a LaunchTimer is installed on the calling thread,
+// every kernel launch of this library takes an event pair from it and goes through
+// hipExtLaunchKernelGGL, which stores that kernel's own start and end times in the two events: no
+// marker between launches and no host synchronization, so a stage's time is its kernels' device
+// time, as a kernel trace reports it.
+struct LaunchTimer {
+  virtual void events(hipEvent_t* start, hipEvent_t* stop) = 0;
+};
+extern thread_local LaunchTimer* g_launch_timer;
+
+#define LAYA_LAUNCH(kernel, grid, block, shmem, stream, ...)                                    \
+  do {                                                                                          \
+    if (laya::g_launch_timer) {                                                                 \
+      hipEvent_t ev_a_, ev_b_;                                                                  \
+      laya::g_launch_timer->events(&ev_a_, &ev_b_);                                             \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ev_a_, ev_b_, 0u, __VA_ARGS__); \
+    } else {                                                                                    \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                      \
+    }                                                                                           \
+  } while (0)
 
 typedef uint16_t bf16_t;                       // bf16 bit pattern in memory
 

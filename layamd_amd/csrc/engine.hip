@@ -46,26 +46,53 @@ namespace laya {
 static int env_int(const char* n, int d) { const char* s = getenv(n); return s && *s ? atoi(s) : d; }
 
 // ---------------------------------------------------------------- profiling
-struct Prof {
+thread_local LaunchTimer* g_launch_timer = nullptr;
+
+// Per-stage device time, as the reference's stage profiler reports it (src/engine.hip:35-47), but
+// measured per kernel: between begin() and end() this is the calling thread's LaunchTimer, so each
+// of the stage's launches records its own start and end into an event pair from the pool.  Nothing
+// waits during the pass; collect() (after the stream has been synchronized) reads the pairs and
+// adds each kernel's duration to its stage.
+struct Prof : LaunchTimer {
   bool on = false;
-  hipEvent_t a = nullptr, b = nullptr;
-  std::vector<std::tuple<std::string, double, long long>> acc;
+  std::vector<std::tuple<std::string, double, long long>> acc;   // stage, ms, stage executions
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pool;
+  std::vector<std::pair<size_t, size_t>> pending;                  // (acc index, pool index)
+  size_t cur = 0;
   void init() {
-    LAYA_HIP(hipEventCreate(&a));
-    LAYA_HIP(hipEventCreate(&b));
     const char* p = getenv("LAYA_PROFILE");
     on = p != nullptr && *p && strcmp(p, "0") != 0;
   }
-  void start(hipStream_t st) { if (on) LAYA_HIP(hipEventRecord(a, st)); }
-  void stop(const char* name, hipStream_t st) {
+  void events(hipEvent_t* a, hipEvent_t* b) override {
+    const size_t i = pending.size();
+    if (i == pool.size()) {
+      hipEvent_t x, y;
+      LAYA_HIP(hipEventCreate(&x));
+      LAYA_HIP(hipEventCreate(&y));
+      pool.emplace_back(x, y);
+    }
+    pending.emplace_back(cur, i);
+    *a = pool[i].first;
+    *b = pool[i].second;
+  }
+  void begin(const char* name) {
     if (!on) return;
-    LAYA_HIP(hipEventRecord(b, st));
-    LAYA_HIP(hipEventSynchronize(b));
-    float ms = 0.f;
-    LAYA_HIP(hipEventElapsedTime(&ms, a, b));
-    for (auto& e : acc)
-      if (std::get<0>(e) == name) { std::get<1>(e) += ms; std::get<2>(e) += 1; return; }
-    acc.emplace_back(name, (double)ms, 1LL);
+    size_t i = 0;
+    while (i < acc.size() && std::get<0>(acc[i]) != name) i++;
+    if (i == acc.size()) acc.emplace_back(name, 0.0, 0LL);
+    std::get<2>(acc[i]) += 1;
+    cur = i;
+    g_launch_timer = this;
+  }
+  void end() { g_launch_timer = nullptr; }
+  // after the stream has finished every pending launch
+  void collect() {
+    for (const auto& pr : pending) {
+      float ms = 0.f;
+      LAYA_HIP(hipEventElapsedTime(&ms, pool[pr.second].first, pool[pr.second].second));
+      std::get<1>(acc[pr.first]) += ms;
+    }
+    pending.clear();
   }
   void report(int iters) {
     if (acc.empty()) { printf("[laya] profile is empty (set LAYA_PROFILE or call laya_ext_prof_enable)\n"); return; }
@@ -78,7 +105,7 @@ struct Prof {
     for (auto& e : v)
       printf("%-28s %10.4f %8lld %6.1f%%\n", std::get<0>(e).c_str(), std::get<1>(e) / iters, std::get<2>(e),
              100.0 * std::get<1>(e) / tot);
-    printf("%-28s %10.4f (serialized sum)\n", "TOTAL", tot / iters);
+    printf("%-28s %10.4f (serialized sum of kernel time)\n", "TOTAL", tot / iters);
   }
 };
 
@@ -115,7 +142,7 @@ struct Engine : EngineIface {
   PackLimits lim;
   PassCaps caps{};
   bool use_graphs = true, capturing = false, verbose = false;
-  const char* dump_dir = nullptr;
+  std::string dump_dir;                       // LAYA_DUMP_DIR at laya_create (empty: no dumps)
 
   // weights
   T* tok_emb = nullptr;
@@ -330,7 +357,9 @@ struct Engine : EngineIface {
     for (int i = 0; i < cfg.n_layers; i++) {
       const std::string p = "encoder.layers." + std::to_string(i) + ".";
       if (st.get(p + "attn_norm.weight") || i > 0) enc[i].attn_norm = up_f32(st, p + "attn_norm.weight", {D});
-      if (fold_ln && enc[i].attn_norm)
+      // layer 0's attn_norm (optional in a checkpoint) runs as its own LayerNorm after the
+      // embeddings, so only later layers' are folded into Wqkv
+      if (fold_ln && enc[i].attn_norm && i > 0)
         enc[i].Wqkv = up_mat_ln(st, p + "attn.Wqkv.weight", 3 * D, D, p + "attn_norm.weight", "", &enc[i].c_qkv, nullptr);
       else
         enc[i].Wqkv = up_mat(st, p + "attn.Wqkv.weight", 3 * D, D);
@@ -396,9 +425,30 @@ struct Engine : EngineIface {
     lim.pad_id = cfg.pad_id;
     if (cfg.pad_id < 0 || cfg.pad_id >= V) { fprintf(stderr, "[laya] pad_token_id outside the vocabulary\n"); exit(1); }
     lim.pass_tokens = std::max(env_int("LAYA_MAX_TOKENS", 65536), cfg.max_len);
+    {
+      // The kernels read their row operands through buffer resources with 32-bit offsets: every
+      // [rows][width] activation (width up to max(D, I, head FFN)) and V^T must stay below 2 GiB,
+      // with room for a pass's bucket padding.  Larger capacities are capped here.
+      const int64_t width = std::max<int64_t>({(int64_t)D, (int64_t)I, (int64_t)FF});
+      const int64_t cap = (((int64_t)1 << 31) - (1 << 20)) / ((int64_t)sizeof(T) * width) / 64 * 64 - 1024;
+      if (lim.pass_tokens > cap) {
+        fprintf(stderr, "[laya] LAYA_MAX_TOKENS=%d exceeds what 32-bit buffer offsets reach for this model; using %lld\n",
+                lim.pass_tokens, (long long)cap);
+        lim.pass_tokens = (int)cap;
+      }
+    }
     lim.pass_tokens = std::min(std::max(env_int("LAYA_PASS_TOKENS", lim.pass_tokens), cfg.max_len), lim.pass_tokens);
     lim.max_seqs = std::max(1, env_int("LAYA_MAX_SEQS", 512));
     lim.max_grows = std::max(env_int("LAYA_MAX_GATHERED", 32768), kMaxMarkers + 1);
+    {
+      // the gathered rows feed the same kernels (head FFN width), under the same 2 GiB bound
+      const int64_t cap = (((int64_t)1 << 31) - (1 << 20)) / ((int64_t)sizeof(T) * std::max(D, FF)) / 64 * 64 - 1024;
+      if (lim.max_grows > cap) {
+        fprintf(stderr, "[laya] LAYA_MAX_GATHERED=%d exceeds what 32-bit buffer offsets reach; using %lld\n",
+                lim.max_grows, (long long)cap);
+        lim.max_grows = (int)cap;
+      }
+    }
     // attention query tiles: 64 queries (two waves in bf16); LAYA_ATTN_QTILE=128 gives bf16 128-query
     // tiles of four waves, same bits, measured slower on sliding-window layers
     lim.q_tile = sizeof(T) == 2 && env_int("LAYA_ATTN_QTILE", 64) == 128 ? 128 : 64;
@@ -412,8 +462,10 @@ struct Engine : EngineIface {
     caps = pass_caps(lim);
     MT = caps.rows; RG = caps.grows; VTC = (MT + 64 + 63) / 64 * 64;
     x = dalloc<float>((size_t)MT * D);
-    xn = dalloc<T>((size_t)MT * D); q = dalloc<T>((size_t)MT * D); k = dalloc<T>((size_t)MT * D);
-    ao = dalloc<T>((size_t)MT * D);
+    // zeroed once: rows that no kernel of a pass writes (bucket padding after the last question, the
+    // attention output of padding rows) are still read, with weight 0, and must hold finite values
+    xn = dalloc<T>((size_t)MT * D, true); q = dalloc<T>((size_t)MT * D, true); k = dalloc<T>((size_t)MT * D, true);
+    ao = dalloc<T>((size_t)MT * D, true);
     vt = dalloc<T>((size_t)D * VTC, true);      // zeroed once: unread gaps must stay finite
     mg = dalloc<T>((size_t)MT * I);
     ff = dalloc<T>((size_t)std::max(MT, RG) * FF);
@@ -460,8 +512,7 @@ struct Engine : EngineIface {
         pin_tail = tail;
       }
     }
-    dump_dir = getenv("LAYA_DUMP_DIR");
-    if (dump_dir && !*dump_dir) dump_dir = nullptr;
+    if (const char* dd = getenv("LAYA_DUMP_DIR")) dump_dir = dd;
     LAYA_HIP(hipDeviceSynchronize());
     printf("[laya] ready: rows/pass=%lld gathered rows/pass=%lld graphs=%d\n", (long long)MT, (long long)RG,
            (int)use_graphs);
@@ -510,11 +561,11 @@ struct Engine : EngineIface {
   }
 
   void dump(const char* name, const float* dev, size_t rows) {
-    if (!dump_dir || capturing || collecting) return;
+    if (dump_dir.empty() || capturing || collecting) return;
     LAYA_HIP(hipStreamSynchronize(stream));
     std::vector<float> buf(rows * cfg.d);
     LAYA_HIP(hipMemcpy(buf.data(), dev, buf.size() * 4, hipMemcpyDeviceToHost));
-    std::string fn = std::string(dump_dir) + "/" + name + ".bin";
+    std::string fn = dump_dir + "/" + name + ".bin";
     FILE* f = fopen(fn.c_str(), "wb");
     if (f) { fwrite(buf.data(), 4, buf.size(), f); fclose(f); }
   }
@@ -676,8 +727,8 @@ struct Engine : EngineIface {
     h2d(d_blob, h_blob, blob_layout(s).total);
 
     // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
-#define STAGE(name, ...) do { if (!collecting) { prof.start(st); __VA_ARGS__; prof.stop(name, st); } } while (0)
-#define GSTAGE(name, ...) do { if (collecting) { __VA_ARGS__; } else { prof.start(st); __VA_ARGS__; prof.stop(name, st); } } while (0)
+#define STAGE(name, ...) do { if (!collecting) { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
+#define GSTAGE(name, ...) do { if (collecting) { __VA_ARGS__; } else { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
     STAGE("enc:embed_ln", launch_layernorm<T, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
                                                  nullptr, x, enc[0].attn_norm ? nullptr : xn, st));
     dump("emb", x, T_);
@@ -730,7 +781,7 @@ struct Engine : EngineIface {
         if (fold_ln && !last_layer)
           STAGE("enc:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
       }
-      if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "enc%d", L); dump(nm, x, T_); }
+      if (!dump_dir.empty() && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "enc%d", L); dump(nm, x, T_); }
       if (!last_layer) {
         if (!fold_ln)
           STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, enc[L + 1].attn_norm, nullptr, nullptr,
@@ -774,7 +825,7 @@ struct Engine : EngineIface {
           if (fold_ln) fold_out(g);
           GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
         if (fold_ln) STAGE("head:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
-        if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
+        if (!dump_dir.empty() && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }
       } else {
         // queries, out-proj and FFN only for the R = KT + B rows read afterwards
         STAGE("head:attn_gathered", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, aog, D, d_gtiles, s.ngt(), kQTile, H, d_soff,
@@ -788,7 +839,7 @@ struct Engine : EngineIface {
           GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
         { GemmArgs g = gemm_args(ff, FF, hl.l2W, R, D, FF, hl.l2B); g.X = xg; g.ldx = D; splitk(g);
           GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
-        if (dump_dir && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d_gathered", L); dump(nm, xg, R); }
+        if (!dump_dir.empty() && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d_gathered", L); dump(nm, xg, R); }
       }
     }
     // scorer on the KT marker rows: LN(+bias) -> Linear + GELU -> Linear(D -> 1)
@@ -809,7 +860,7 @@ struct Engine : EngineIface {
   // graph replay on a hit; on a miss run eagerly, then capture the same sequence
   void execute(const Shape& s) {
     last = s; have_last = true;
-    const bool graphs_on = use_graphs && !prof.on && !dump_dir;
+    const bool graphs_on = use_graphs && !prof.on && dump_dir.empty();
     if (graphs_on) {
       auto it = graphs.find(s);
       if (it != graphs.end()) {
@@ -821,6 +872,7 @@ struct Engine : EngineIface {
     tune_pass(s);
     run(s);
     LAYA_HIP(hipStreamSynchronize(stream));
+    if (prof.on) prof.collect();
     if (!graphs_on || graphs.size() >= max_graphs) return;
     hipGraph_t g;
     hipGraphExec_t ex;
@@ -865,7 +917,7 @@ struct Engine : EngineIface {
     LAYA_HIP(hipEventCreate(&a));
     LAYA_HIP(hipEventCreate(&b));
     auto it = graphs.find(last);
-    const bool g = use_graphs && !prof.on && !dump_dir && it != graphs.end();
+    const bool g = use_graphs && !prof.on && dump_dir.empty() && it != graphs.end();
     LAYA_HIP(hipEventRecord(a, stream));
     for (int i = 0; i < iters; i++) {
       if (g) LAYA_HIP(hipGraphLaunch(it->second, stream));
@@ -876,6 +928,7 @@ struct Engine : EngineIface {
     LAYA_HIP(hipEventElapsedTime(ms, a, b));
     LAYA_HIP(hipEventDestroy(a));
     LAYA_HIP(hipEventDestroy(b));
+    if (prof.on) prof.collect();
     return 0;
   }
 
@@ -920,7 +973,7 @@ float laya_temperature(void* h, int qtype) {
   return qtype >= 0 && qtype < (int)t.size() ? t[qtype] : 1.0f;
 }
 void laya_prof_report(void* h, int iters) { E(h)->prof.report(iters); }
-void laya_prof_reset(void* h) { E(h)->prof.acc.clear(); }
+void laya_prof_reset(void* h) { E(h)->prof.acc.clear(); E(h)->prof.pending.clear(); }
 void laya_tune_all(void* h) { E(h)->tune_all(); }
 
 int laya_ext_prof_enable(void* h, int on) { int was = E(h)->prof.on; E(h)->prof.on = on != 0; return was; }
@@ -1008,6 +1061,9 @@ int laya_ext_stats(void* h, long long* out, int n) {
   return 0;
 }
 
+// largest K or V^T operand (bytes) of the attention kernels, whose buffer offsets are 32-bit
+static constexpr size_t kMaxAttnOperandBytes = (size_t)1 << 31;
+
 int laya_ext_attention(int dtype, const void* Q, const void* K, int ldqk, int kv_rows, const void* Vt, int ldv, void* O,
                        int ldo, const int* tiles, int ntiles, int qtile, int H, const int* soff, const int* vlen,
                        const int* gq, const int* grow, int window_half, float scale, void* stream) {
@@ -1016,8 +1072,13 @@ int laya_ext_attention(int dtype, const void* Q, const void* K, int ldqk, int kv
   if ((dtype != 0 && dtype != 1) || !Q || !K || !Vt || !O || !tiles || !soff || !vlen || ntiles < 0 || H < 1 ||
       kv_rows < 1 || window_half < 0 || !(scale > 0.f) || (gq == nullptr) != (grow == nullptr))
     return -1;
-  if (qtile != 64 && !(qtile == 128 && dtype == 1 && !gq)) return -1;
+  // 128-query tiles: bf16, not gathered, and a window (if any) whose half width is a multiple of the
+  // 64-key block; the gathered mode attends to every key of the question (no window)
+  if (qtile != 64 && !(qtile == 128 && dtype == 1 && !gq && window_half % 64 == 0)) return -1;
+  if (gq && window_half > 0) return -1;
   if (ldqk < H * 64 || ldo < H * 64 || ldv < 64 || (ldqk * elt) % 16 || (ldo * elt) % 16 || (ldv * elt) % 16) return -1;
+  // K and V^T are read through buffer resources with 32-bit record counts and offsets
+  if ((size_t)kv_rows * ldqk * elt >= kMaxAttnOperandBytes || (size_t)H * 64 * ldv * elt >= kMaxAttnOperandBytes) return -1;
   if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) | reinterpret_cast<uintptr_t>(Vt) |
        reinterpret_cast<uintptr_t>(O)) & 15)
     return -1;

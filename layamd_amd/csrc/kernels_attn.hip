@@ -512,13 +512,13 @@ void launch_attention(const T* Q, const T* K, int ldqk, int kv_rows, const T* Vt
   }
   if constexpr (sizeof(T) == 2) {
     if (qtile == 128)
-      hipLaunchKernelGGL(k_attention_bf16<4>, dim3(H, ntiles), dim3(256), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
+      LAYA_LAUNCH(k_attention_bf16<4>, dim3(H, ntiles), dim3(256), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
                          ldo, tiles, soff, vlen, gq, grow, window_half, scale);
     else
-      hipLaunchKernelGGL(k_attention_bf16<2>, dim3(H, ntiles), dim3(128), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
+      LAYA_LAUNCH(k_attention_bf16<2>, dim3(H, ntiles), dim3(128), 0, st, Q, K, ldqk, kv_rows, Vt, ldv, H * 64, O,
                          ldo, tiles, soff, vlen, gq, grow, window_half, scale);
   } else {
-    hipLaunchKernelGGL((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
+    LAYA_LAUNCH((k_attention<T>), dim3(ntiles, H), dim3(256), 0, st, Q, K, ldqk, Vt, ldv, O, ldo, tiles, soff,
                        vlen, gq, grow, window_half, scale);
   }
 }

@@ -254,10 +254,10 @@ template <typename T, int BM, int BN, int WM, int WN>
 static void launch_cfg(int epi, const GemmArgs& a, hipStream_t st) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, EPI_STORE>), dim3(tiles), dim3(256), 0, st, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, EPI_RESID>), dim3(tiles), dim3(256), 0, st, a); break;
-    case EPI_QKV: hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, EPI_QKV>), dim3(tiles), dim3(256), 0, st, a); break;
-    case EPI_GEGLU: hipLaunchKernelGGL((k_gemm<T, BM, BN, WM, WN, EPI_GEGLU>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_STORE: LAYA_LAUNCH((k_gemm<T, BM, BN, WM, WN, EPI_STORE>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_RESID: LAYA_LAUNCH((k_gemm<T, BM, BN, WM, WN, EPI_RESID>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_QKV: LAYA_LAUNCH((k_gemm<T, BM, BN, WM, WN, EPI_QKV>), dim3(tiles), dim3(256), 0, st, a); break;
+    case EPI_GEGLU: LAYA_LAUNCH((k_gemm<T, BM, BN, WM, WN, EPI_GEGLU>), dim3(tiles), dim3(256), 0, st, a); break;
     default: fprintf(stderr, "[laya] gemm: bad epilogue %d\n", epi); exit(1);
   }
 }
@@ -1323,7 +1323,7 @@ __global__ __launch_bounds__(256) void k_mfma_loop(float* __restrict__ out, int 
 }
 
 void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st) {
-  hipLaunchKernelGGL(k_mfma_loop, dim3(blocks), dim3(256), 0, st, out, iters);
+  LAYA_LAUNCH(k_mfma_loop, dim3(blocks), dim3(256), 0, st, out, iters);
 }
 
 // compute units of the current device, cached per device.  If the query fails (a process whose
@@ -1365,26 +1365,26 @@ static void launch_xl_ring(const GemmArgs& a, int tiles, hipStream_t st) {
     if constexpr (ln_fold_built<EPI, ACT>(true) && (EPI == EPI_RESID || BM * BN < 256 * 256)) {
       const bool hb = EPI == EPI_QKV || a.bias != nullptr;
       if constexpr (EPI == EPI_RESID) {
-        if (hb) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        if (hb) LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        else LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
         return;
       } else if constexpr (EPI == EPI_QKV) {
         // the encoder's projection has no bias; its fold kernel leaves the bias code out
-        if (a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        if (a.bias) LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
+        else LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a);
         return;
       } else if constexpr (EPI == EPI_STORE) {
-        if (hb) { hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
+        if (hb) { LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
       } else {
-        if (!hb) { hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
+        if (!hb) { LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, true>), dim3(tiles), dim3(256), 0, st, a); return; }
       }
     }
     fprintf(stderr, "[laya] gemm: no LayerNorm-fold kernel for epilogue %d, activation %d, bias %d\n", EPI, ACT,
             (int)(a.bias != nullptr));
     exit(1);
   }
-  if (EPI == EPI_QKV || a.bias) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
-  else if constexpr (EPI != EPI_QKV) hipLaunchKernelGGL((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
+  if (EPI == EPI_QKV || a.bias) LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, true, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
+  else if constexpr (EPI != EPI_QKV) LAYA_LAUNCH((k_gemm_xl<BM, BN, WM, WN, EPI, ACT, false, LOOP, false>), dim3(tiles), dim3(256), 0, st, a);
 }
 
 // 128x128 tiles take the three-A-buffer loop when the grid has more tiles than the chip has CUs,
@@ -1460,9 +1460,25 @@ void gemm_pin_split(int split_rows, int cfg_tail) {
   g_cfg_tail.store(cfg_tail, std::memory_order_relaxed);
 }
 
+// Largest operand, in bytes, that any GEMM launch accepts.  The tiled kernel reads A and W through
+// buffer resources whose record count and offsets are 32-bit (it takes operands below 2 GiB,
+// xl_usable, and hands larger ones to the generic kernel); a 4 GiB limit on every operand keeps
+// all byte counts the launchers compute from int shapes exact, whichever kernel runs.
+static constexpr size_t kMaxOperandBytes = (size_t)1 << 32;
+
 bool gemm_shape_ok(int epi, const GemmArgs& a, int elt_bytes, const char** why) {
   const int bk = 128 / elt_bytes, align = 16 / elt_bytes;
   if (a.M <= 0 || a.N <= 0) { *why = "empty"; return false; }
+  {
+    const size_t M = (size_t)a.M, N = (size_t)a.N, e = (size_t)elt_bytes;
+    size_t big = std::max(M * (size_t)std::max(a.lda, 0) * e, N * (size_t)std::max(a.ldw, 0) * e);
+    if (epi == EPI_STORE || epi == EPI_GEGLU) big = std::max(big, M * (size_t)std::max(a.ldc, 0) * e);
+    if (epi == EPI_RESID) big = std::max(big, M * (size_t)std::max(a.ldx, 0) * 4);
+    if (epi == EPI_QKV)
+      big = std::max(big, std::max(M * (size_t)std::max(a.ldqk, 0) * e, N / 3 * (size_t)std::max(a.ldv, 0) * e));
+    if (a.Xh) big = std::max(big, M * (size_t)std::max(a.ldxh, 0) * 2);
+    if (big >= kMaxOperandBytes) { *why = "every operand must be smaller than 4 GiB"; return false; }
+  }
   if (a.K <= 0 || a.K % bk) { *why = "K must be a positive multiple of the 128-byte K slice"; return false; }
   if (a.lda % align || a.ldw % align || a.lda < a.K || a.ldw < a.K) { *why = "row strides must be 16-byte multiples >= K"; return false; }
   if ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W)) & 15) { *why = "operands must be 16-byte aligned"; return false; }
@@ -1614,8 +1630,8 @@ template <int EPI, int ACT>
 static void launch_reduce(const GemmArgs& a, const float* ws, int ks, int M, void* out, int ldo, hipStream_t st) {
   const size_t n4 = (size_t)M * a.N / 4;
   const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-  if (a.bias) hipLaunchKernelGGL((k_splitk_reduce<EPI, ACT, true>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
-  else hipLaunchKernelGGL((k_splitk_reduce<EPI, ACT, false>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
+  if (a.bias) LAYA_LAUNCH((k_splitk_reduce<EPI, ACT, true>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
+  else LAYA_LAUNCH((k_splitk_reduce<EPI, ACT, false>), dim3(blocks), dim3(256), 0, st, ws, ks, M, a.N, a.bias, out, ldo);
 }
 
 // Split-K over rows chunks that fit the workspace: per chunk one launch of ks x tiles workgroups
@@ -1696,8 +1712,8 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     launch_cfg<T, 128, 128, 2, 2>(epi, a, st);
   } else if (tiles64 < num_cus() && (epi == EPI_STORE || epi == EPI_RESID)) {
     const int tiles = ((a.M + 31) / 32) * ((a.N + 63) / 64);
-    if (epi == EPI_STORE) hipLaunchKernelGGL((k_gemm<T, 32, 64, 2, 2, EPI_STORE>), dim3(tiles), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_gemm<T, 32, 64, 2, 2, EPI_RESID>), dim3(tiles), dim3(256), 0, st, a);
+    if (epi == EPI_STORE) LAYA_LAUNCH((k_gemm<T, 32, 64, 2, 2, EPI_STORE>), dim3(tiles), dim3(256), 0, st, a);
+    else LAYA_LAUNCH((k_gemm<T, 32, 64, 2, 2, EPI_RESID>), dim3(tiles), dim3(256), 0, st, a);
   } else {
     launch_cfg<T, 64, 64, 4, 1>(epi, a, st);
   }

@@ -133,10 +133,10 @@ void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float ep
     constexpr bool MR = decltype(mr)::value;
     if (D <= 1024) {
       constexpr int RPW = 2;
-      hipLaunchKernelGGL((k_layernorm<Tin, T, RPW, 4, MR>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x,
+      LAYA_LAUNCH((k_layernorm<Tin, T, RPW, 4, MR>), dim3((rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, st, x,
                          gather, rows, D, eps, w, b, addtab, qt, seq, y32, yT, ymr);
     } else {
-      hipLaunchKernelGGL((k_layernorm<Tin, T, 1, kLnMaxChunks, MR>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows,
+      LAYA_LAUNCH((k_layernorm<Tin, T, 1, kLnMaxChunks, MR>), dim3((rows + 3) / 4), dim3(256), 0, st, x, gather, rows,
                          D, eps, w, b, addtab, qt, seq, y32, yT, ymr);
     }
   };
@@ -188,8 +188,8 @@ void launch_ln_rowstats(const float* stats, int ldst, int G, int rows, float eps
   auto* sp = reinterpret_cast<const float2*>(stats);
   auto* mp = reinterpret_cast<float2*>(mr);
   // one wave per workgroup: the few hundred waves spread over as many CUs
-  if (G <= 16) hipLaunchKernelGGL(k_ln_rowstats<16>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
-  else hipLaunchKernelGGL(k_ln_rowstats<32>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
+  if (G <= 16) LAYA_LAUNCH(k_ln_rowstats<16>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
+  else LAYA_LAUNCH(k_ln_rowstats<32>, dim3((rows + 63) / 64), dim3(64), 0, st, sp, ldst, G, rows, eps, mp);
 }
 
 // Deterministic finite pattern, uniform in [-1, 1), written over n elements (operands for GEMM
@@ -207,7 +207,7 @@ template <typename T>
 void launch_fill_pattern(T* p, size_t n, uint32_t seed, hipStream_t st) {
   if (n == 0) return;
   const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
-  hipLaunchKernelGGL(k_fill_pattern<T>, dim3((unsigned)blocks), dim3(256), 0, st, p, n, seed);
+  LAYA_LAUNCH(k_fill_pattern<T>, dim3((unsigned)blocks), dim3(256), 0, st, p, n, seed);
 }
 template void launch_fill_pattern<float>(float*, size_t, uint32_t, hipStream_t);
 template void launch_fill_pattern<bf16_t>(bf16_t*, size_t, uint32_t, hipStream_t);
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x
 
 void launch_gather_rows(const float* x, const int* rows, float* xg, int R, int D, hipStream_t st) {
   if (R <= 0) return;
-  hipLaunchKernelGGL(k_gather_rows, dim3((R + 3) / 4), dim3(256), 0, st, x, rows, xg, R, D);
+  LAYA_LAUNCH(k_gather_rows, dim3((R + 3) / 4), dim3(256), 0, st, x, rows, xg, R, D);
 }
 
 // ---- scorer tail: one wave per row, fp32 accumulation ----
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void k_row_dot(const T* __restrict__ h, int ld
 template <typename T>
 void launch_row_dot(const T* h, int ldh, const float* w, const float* b, float* logits, int R, int D, hipStream_t st) {
   if (R <= 0) return;
-  hipLaunchKernelGGL((k_row_dot<T>), dim3((R + 3) / 4), dim3(256), 0, st, h, ldh, w, b, logits, R, D);
+  LAYA_LAUNCH((k_row_dot<T>), dim3((R + 3) / 4), dim3(256), 0, st, h, ldh, w, b, logits, R, D);
 }
 template void launch_row_dot<float>(const float*, int, const float*, const float*, float*, int, int, hipStream_t);
 template void launch_row_dot<bf16_t>(const bf16_t*, int, const float*, const float*, float*, int, int, hipStream_t);
@@ -339,8 +339,8 @@ void launch_act_head(const float* cls, int D, const float* logits, const int* mo
                      const float* B0, const float* W2, const float* B2, int n_act, float* out, float* hidden, int B,
                      hipStream_t st) {
   if (B <= 0) return;
-  hipLaunchKernelGGL(k_act_hidden, dim3(B, 16), dim3(256), 0, st, cls, D, logits, moff, nmark, W0, B0, hidden);
-  hipLaunchKernelGGL(k_act_out, dim3(B), dim3(64), 0, st, hidden, W2, B2, n_act, out);
+  LAYA_LAUNCH(k_act_hidden, dim3(B, 16), dim3(256), 0, st, cls, D, logits, moff, nmark, W0, B0, hidden);
+  LAYA_LAUNCH(k_act_out, dim3(B), dim3(64), 0, st, hidden, W2, B2, n_act, out);
 }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));   // one 16-byte chunk
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void k_hbm_copy(const u32x4_t* __restrict__ sr
 }
 
 void launch_hbm_copy(const void* src, void* dst, size_t n16, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL(k_hbm_copy, dim3(blocks), dim3(256), 0, st, static_cast<const u32x4_t*>(src),
+  LAYA_LAUNCH(k_hbm_copy, dim3(blocks), dim3(256), 0, st, static_cast<const u32x4_t*>(src),
                      static_cast<u32x4_t*>(dst), n16);
 }
 

@@ -10,7 +10,9 @@
 // captures a graph), the second replays it.  Per question it reports max |dlogit|, max |dprob| of
 // the softmax over its markers and max |dact| / max(1, |act|); a question passes when dprob <= P
 // (default 0.01, the reference tool's bar), dact <= A (default 0.05) and dlogit <= L (default: no
-// bound).  Exit status 0 when every question passes, 1 otherwise, 2 on a bad input.
+// bound), and every engine logit and act value is finite.  Exit status 0 when every question
+// passes, 1 otherwise, 2 on a bad input.  `laya-parity --self-check` runs the comparison on planted
+// values (NaN, Inf, out-of-bar) without an engine.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -50,9 +52,67 @@ void softmax(const float* z, int k, std::vector<double>* p) {
   for (int i = 0; i < k; i++) (*p)[i] /= s;
 }
 
+// running maximum that keeps a NaN once one is seen (std::max(acc, NaN) would return acc)
+double worse(double acc, double x) { return std::isnan(acc) || std::isnan(x) ? NAN : std::max(acc, x); }
+
+struct QuestionDiff {
+  double dl = 0.0, dp = 0.0, da = 0.0;
+  bool finite = true;                    // every engine logit and act value is finite
+};
+
+// One question: K engine logits lo against golden gl, n_act act values against gact.
+QuestionDiff compare_question(const float* lo, const float* gl, int K, const float* act, const float* gact, int n_act) {
+  QuestionDiff q;
+  for (int i = 0; i < K; i++) q.finite = q.finite && std::isfinite(lo[i]);
+  for (int i = 0; i < n_act; i++) q.finite = q.finite && std::isfinite(act[i]);
+  std::vector<double> pe, pg;
+  softmax(lo, K, &pe);
+  softmax(gl, K, &pg);
+  for (int i = 0; i < K; i++) {
+    q.dl = worse(q.dl, std::fabs((double)lo[i] - gl[i]));
+    q.dp = worse(q.dp, std::fabs(pe[i] - pg[i]));
+  }
+  for (int i = 0; i < n_act; i++) {
+    const double g = gact[i];
+    q.da = worse(q.da, std::fabs(act[i] - g) / std::max(1.0, std::fabs(g)));
+  }
+  return q;
+}
+
+// A question passes only with finite engine outputs and every difference within its bar (a NaN
+// difference compares false, so it fails too).
+bool question_passes(const QuestionDiff& q, double prob_tol, double act_tol, double logit_tol) {
+  return q.finite && q.dp <= prob_tol && q.da <= act_tol && q.dl <= logit_tol;
+}
+
+// --self-check: the comparison on planted values, no engine or GPU involved.  Exit 0 when a clean
+// question passes and NaN, +-Inf or out-of-bar values in logits or act values each fail.
+int self_check() {
+  const float gl[3] = {0.1f, -0.2f, 0.3f}, ga[2] = {1.0f, -2.0f};
+  auto run = [&](const float* lo, const float* act) {
+    return question_passes(compare_question(lo, gl, 3, act, ga, 2), 0.01, 0.05, INFINITY);
+  };
+  const float ok_lo[3] = {0.1f, -0.2f, 0.3001f}, ok_act[2] = {1.0f, -2.0f};
+  const float nan_lo[3] = {0.1f, NAN, 0.3f}, inf_lo[3] = {INFINITY, -0.2f, 0.3f}, ninf_lo[3] = {0.1f, -INFINITY, 0.3f};
+  const float nan_act[2] = {1.0f, NAN}, inf_act[2] = {INFINITY, -2.0f}, far_lo[3] = {2.0f, -0.2f, 0.3f};
+  const float far_act[2] = {1.5f, -2.0f};
+  int bad = 0;
+  bad += !run(ok_lo, ok_act);
+  bad += run(nan_lo, ok_act);
+  bad += run(inf_lo, ok_act);
+  bad += run(ninf_lo, ok_act);
+  bad += run(ok_lo, nan_act);
+  bad += run(ok_lo, inf_act);
+  bad += run(far_lo, ok_act);
+  bad += run(ok_lo, far_act);
+  printf("laya-parity self-check: %s\n", bad ? "FAILED" : "ok");
+  return bad ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+  if (argc == 2 && strcmp(argv[1], "--self-check") == 0) return self_check();
   if (argc < 3) {
     fprintf(stderr, "usage: laya-parity <model_dir> <golden_dir> [--prob-tol P] [--act-tol A] [--logit-tol L]\n");
     return 2;
@@ -117,26 +177,14 @@ int main(int argc, char** argv) {
       size_t off = 0;
       for (int q = 0; q < n; q++) {
         const int K = nmark[q];
-        const float* lo = logits.data() + off;
-        const float* gl = glog.data() + (size_t)q * kmax;
-        std::vector<double> pe, pg;
-        softmax(lo, K, &pe);
-        softmax(gl, K, &pg);
-        double dl = 0.0, dp = 0.0, da = 0.0;
-        for (int i = 0; i < K; i++) {
-          dl = std::max(dl, std::fabs((double)lo[i] - gl[i]));
-          dp = std::max(dp, std::fabs(pe[i] - pg[i]));
-        }
-        for (int i = 0; i < n_act; i++) {
-          const double g = gact[(size_t)q * n_act + i];
-          da = std::max(da, std::fabs(act[(size_t)q * n_act + i] - g) / std::max(1.0, std::fabs(g)));
-        }
-        const bool ok = dp <= prob_tol && da <= act_tol && dl <= logit_tol;
+        const QuestionDiff d = compare_question(logits.data() + off, glog.data() + (size_t)q * kmax, K,
+                                                act.data() + (size_t)q * n_act, gact.data() + (size_t)q * n_act, n_act);
+        const bool ok = question_passes(d, prob_tol, act_tol, logit_tol);
         total++;
         failed += !ok;
-        worst_p = std::max(worst_p, dp); worst_l = std::max(worst_l, dl); worst_a = std::max(worst_a, da);
+        worst_p = worse(worst_p, d.dp); worst_l = worse(worst_l, d.dl); worst_a = worse(worst_a, d.da);
         printf("%-22s %4d %5d %4d %12.3e %12.3e %12.3e  %s\n", (name + (round ? " (replay)" : "")).c_str(), q, lens[q], K,
-               dl, dp, da, ok ? "pass" : "FAIL");
+               d.dl, d.dp, d.da, ok ? "pass" : (d.finite ? "FAIL" : "FAIL (non-finite output)"));
         off += K;
       }
     }

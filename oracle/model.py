@@ -115,7 +115,9 @@ def forward(W: Weights, cfg, input_ids, attention_mask, marker_pos, marker_mask,
     for i in range(cfg.n_layers):
         p = "encoder.layers.%d." % i
         glob = cfg.is_global(i)
-        h = x if i == 0 else ln(x, W[p + "attn_norm.weight"])
+        # layer 0 has no attn_norm in HF ModernBERT (Identity); the reference engine applies one
+        # when a checkpoint carries it (src/engine.hip:154-155, 415)
+        h = ln(x, W[p + "attn_norm.weight"]) if (i > 0 or W.get(p + "attn_norm.weight") is not None) else x
         qkv = (h @ W[p + "attn.Wqkv.weight"].T).view(n, L, 3, H, HD)
         q, k, v = (qkv[:, :, j].transpose(1, 2) for j in range(3))
         c, s = (cos_g, sin_g) if glob else (cos_l, sin_l)

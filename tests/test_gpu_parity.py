@@ -641,9 +641,13 @@ def test_gemm_tuning_keeps_outputs():
 
 
 # questions of the bf16 benchmark batches with the reference's bf16 drift recorded
-# (tests/golden/<tag>/drift.npz, written by make_golden.py): (checkpoint preset, batch, questions)
+# (tests/golden/<tag>/drift.npz, written by make_golden.py): (checkpoint preset, batch, questions);
+# the *_full records hold every question of the b32 x s512 and b16 x s1024 batches
 SAMPLES = {"c3_sample": ("large", wl.c3, [0, 1, 2, 3]), "c4_sample": ("base", wl.c4, [11, 15]),
-           "c5_sample": ("large1024", wl.c5, [50, 17, 24])}
+           "c5_sample": ("large1024", wl.c5, [50, 17, 24]),
+           "c3_full": ("large", wl.c3, list(range(32))), "c4_full": ("base", wl.c4, list(range(16)))}
+# for a whole-batch record, the sample whose questions must give the same bits inside the full pass
+SUBSET_OF_FULL = {"c3_full": "c3_sample", "c4_full": "c4_sample"}
 
 
 @pytest.mark.parametrize("tag", list(SAMPLES))
@@ -651,15 +655,18 @@ def test_bf16_sample_layer_drift(tag):
     """bf16 engine on questions of the b32 x s512 (ModernBERT-large), b16 x s1024 (mmBERT-base) and
     b64 varlen (ModernBERT-large-1024, 25-29 markers per sequence) batches: every valid row of every
     layer against the fp32 CPU oracle, within BF16_VS_UPSTREAM times the reference's own bf16 drift
-    on the same questions; logits and act logits likewise.  For the varlen batch the whole
-    64-sequence pass (18k tokens) must give the same bits for these questions."""
+    on the same questions; logits and act logits likewise.  The c3_full and c4_full records cover
+    every question of the b32 x s512 and b16 x s1024 batches (C3's longest question has 510
+    tokens), run as the one pass bench.py times; the sampled questions must give the same bits
+    inside that pass as in their own.  For the varlen batch the whole 64-sequence pass (18k tokens)
+    must give the same bits for the sampled questions."""
     import torch
     from oracle import model as om
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     preset, make, pick = SAMPLES[tag]
     ref = np.load(os.path.join(GOLDEN, tag, "drift.npz"))
     full = make(0)
-    b = full.subset(pick)
+    b = full.subset(pick) if len(pick) < full.B else full
     assert list(ref["lens"]) == list(b.lens)
     d = ck.cached_checkpoint(preset)
     cfg, W = ck.load_checkpoint(d)
@@ -669,11 +676,13 @@ def test_bf16_sample_layer_drift(tag):
     up_lo = np.concatenate([ref["logits_bf16_autocast"][i, :nm[i]] - ref["logits"][i, :nm[i]] for i in range(b.B)])
     dl_up = float(np.abs(up_lo).max())
     da_up = float(np.abs(ref["act_logits_bf16_autocast"] - ref["act_logits"]).max())
+    max_tokens = max(8192, int(np.sum((lens + 7) // 8 * 8)) + 1024)
     # the c3 sample also runs the LayerNorm fold (LAYA_LN_FOLD=1), against the same budgets
     for fold in ((0, 1) if tag == "c3_sample" else (0,)):
         worst = (0.0, "")
         with tempfile.TemporaryDirectory() as dd:
-            e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0, LAYA_LN_FOLD=fold))
+            e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0, LAYA_LN_FOLD=fold,
+                                                              LAYA_MAX_TOKENS=max_tokens))
             lo_f, ac_f = e.forward_flat(lens, ids, nm, mk, qt)
             for li, name in enumerate(ref["layers"]):
                 got = _dump_rows(dd, {"final_norm": "final"}.get(str(name), str(name)), cfg.d)
@@ -702,3 +711,37 @@ def test_bf16_sample_layer_drift(tag):
         got = np.concatenate([flo[moff[i]:moff[i + 1]] for i in pick])
         assert np.array_equal(got, e.forward_flat(lens, ids, nm, mk, qt)[0]) and np.array_equal(got, lo)
         assert np.array_equal(fac.reshape(64, -1)[pick], ac.reshape(len(pick), -1))
+    if tag in SUBSET_OF_FULL:
+        # the sampled questions, run as their own pass, give the bits they have inside the full pass
+        sub = SAMPLES[SUBSET_OF_FULL[tag]][2]
+        bs = full.subset(sub)
+        e = le.Engine(None, d, precision="bf16", env=dict(ENV, LAYA_MAX_TOKENS=max_tokens))
+        assert np.array_equal(e.forward_flat(*b.flat())[0], lo)        # graph replay of the full pass: same bits
+        slo, sac = e.forward_flat(*bs.flat())
+        moff = np.concatenate([[0], np.cumsum(full.nmark)])
+        assert np.array_equal(np.concatenate([lo[moff[i]:moff[i + 1]] for i in sub]), slo)
+        assert np.array_equal(ac.reshape(full.B, -1)[sub], sac.reshape(len(sub), -1))
+
+
+@pytest.mark.parametrize("tag", ["c3_full", "c4_full"])
+def test_fp32_full_batch_vs_reference(tag):
+    """fp32 engine on every question of the b32 x s512 (ModernBERT-large) and b16 x s1024
+    (mmBERT-base) batches in one pass, against the logits and act logits the reference's own fp32
+    PyTorch model produced for the same inputs (tests/golden/<tag>/drift.npz): probabilities within
+    1e-4 and act logits within 1e-3 (relative, |x| >= 1), the fp32 bars."""
+    preset, make, _ = SAMPLES[tag]
+    ref = np.load(os.path.join(GOLDEN, tag, "drift.npz"))
+    b = make(0)
+    assert list(ref["lens"]) == list(b.lens)
+    lens, ids, nm, mk, qt = b.flat()
+    e = le.Engine(None, ck.cached_checkpoint(preset), precision="fp32",
+                  env=dict(ENV, LAYA_MAX_TOKENS=max(8192, int(np.sum((lens + 7) // 8 * 8)) + 1024)))
+    lo, ac = e.forward_flat(lens, ids, nm, mk, qt)
+    ref_lo = np.concatenate([ref["logits"][i, :nm[i]] for i in range(b.B)])
+    dp = prob_delta(lo, ref_lo, nm)
+    dl = float(np.abs(lo - ref_lo).max())
+    da = float((np.abs(ac.reshape(b.B, -1) - ref["act_logits"]) / np.maximum(1.0, np.abs(ref["act_logits"]))).max())
+    print("%s fp32, %d questions, %d tokens: max|dprob| %.2e, max|dlogit| %.2e, rel|dact| %.2e"
+          % (tag, b.B, int(lens.sum()), dp, dl, da))
+    assert np.isfinite(lo).all() and np.isfinite(ac).all()
+    assert dp <= 1e-4 and da <= 1e-3

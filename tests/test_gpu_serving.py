@@ -204,3 +204,89 @@ def test_cpp_latency_tool():
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
     print(r.stdout[-4000:])
     assert r.returncode == 0 and "batched" in r.stdout
+
+
+def _with_layer0_attn_norm(src_dir, out_dir, w):
+    """A copy of the checkpoint in src_dir that also carries encoder.layers.0.attn_norm.weight = w,
+    the tensor the reference engine treats as optional (src/engine.hip:154-155, 415)."""
+    import shutil
+    os.makedirs(os.path.join(out_dir, "encoder"), exist_ok=True)
+    shutil.copy(os.path.join(src_dir, "encoder", "config.json"), os.path.join(out_dir, "encoder", "config.json"))
+    shutil.copy(os.path.join(src_dir, "rl_agent_config.json"), os.path.join(out_dir, "rl_agent_config.json"))
+    _, W = ck.load_checkpoint(src_dir)
+    W["encoder.layers.0.attn_norm.weight"] = w
+    names = list(W)
+    ck.write_safetensors(os.path.join(out_dir, "model.safetensors"), [(n, W[n].shape) for n in names],
+                         lambda i: W[names[i]], "F32")
+    return out_dir
+
+
+def test_layer0_attn_norm_with_and_without_fold(tmp_path):
+    """A checkpoint with a layer-0 attn_norm (weight 2 + 0.5 N(0,1)): the weight is applied once, by
+    the explicit LayerNorm after the embeddings, with the LayerNorm fold on or off.  The first
+    layer's output (LAYA_DUMP_DIR) of the fp32 engine matches the fp32 oracle, which applies that
+    LayerNorm too, and both bf16 engines stay within the tiny model's bf16 bar (2.5e-2 of the row
+    RMS); leaving the LayerNorm out or applying its weight twice moves that output by more than 3x
+    the bar, so the check sees either mistake.  Logits: fp32 bars, and 2e-3 for bf16."""
+    import tempfile
+    from oracle import model as om
+    tiny = ck.PRESETS["tiny"]
+    D = tiny.d
+    w = (2.0 + 0.5 * np.random.default_rng(5).standard_normal(D)).astype(np.float32)
+    d = _with_layer0_attn_norm(checkpoint_dir("tiny"), str(tmp_path / "l0norm"), w)
+    cfg, W = ck.load_checkpoint(d)
+    b = wl.make_batch(tiny, [5, 64, 129, 320], [2, 3, 12, 4], seed=11)
+    ids, att, mp, mm, qt = b.padded()
+    valid = att.astype(bool)
+
+    def oracle_enc0(Wd):
+        cap = {}
+        lo, ac = om.forward(om.Weights(Wd), tiny, ids, att, mp, mm.astype(bool), qt, capture=cap)
+        return cap["enc0"].numpy().astype(np.float64), lo.numpy(), ac.numpy()
+    ref0, ref_lo_pad, ref_ac = oracle_enc0(W)
+    ref_lo = np.concatenate([ref_lo_pad[i, :b.nmark[i]] for i in range(b.B)])
+    rms = np.sqrt((ref0 ** 2).mean(-1))
+    rel = lambda a: float((np.abs(a - ref0).max(-1) / rms)[valid].max())
+    bar = 2.5e-2
+    wrong = {"none": dict(W), "twice": dict(W, **{"encoder.layers.0.attn_norm.weight": w * w})}
+    del wrong["none"]["encoder.layers.0.attn_norm.weight"]
+    for k, Wd in wrong.items():
+        r = rel(oracle_enc0(Wd)[0])
+        print("oracle with the layer-0 LayerNorm %s: enc0 moves %.4f of the row RMS" % (k, r))
+        assert r > 3 * bar, k
+    lens = b.lens
+    soff = np.concatenate([[0], np.cumsum((lens + 7) // 8 * 8)])
+
+    def engine_enc0(prec, **env):
+        with tempfile.TemporaryDirectory() as dd:
+            lo, ac = make_engine(d, prec, LAYA_DUMP_DIR=dd, LAYA_GRAPHS=0, **env).forward_flat(*b.flat())
+            got = np.fromfile(os.path.join(dd, "enc0.bin"), dtype=np.float32).reshape(-1, D)
+        e0 = np.zeros_like(ref0)
+        for i in range(b.B):
+            e0[i, :lens[i]] = got[soff[i]:soff[i] + lens[i]]
+        return e0, lo, ac
+    e0, lo32, ac32 = engine_enc0("fp32")
+    print("fp32: enc0 %.2e of the row RMS, max|dlogit| %.2e" % (rel(e0), np.abs(lo32 - ref_lo).max()))
+    assert rel(e0) < 1e-4
+    assert np.abs(lo32 - ref_lo).max() < 1e-4
+    assert (np.abs(ac32 - ref_ac) / np.maximum(1.0, np.abs(ref_ac))).max() < 1e-3
+    out = {}
+    for fold in (0, 1):
+        e0, lo, ac = engine_enc0("bf16", LAYA_LN_FOLD=fold)
+        print("bf16 fold %d: enc0 %.4f of the row RMS, max|dlogit| %.2e" % (fold, rel(e0), np.abs(lo - ref_lo).max()))
+        assert rel(e0) < bar, fold
+        assert np.abs(lo - ref_lo).max() < 2e-3, fold
+        out[fold] = lo
+    assert np.abs(out[0] - out[1]).max() < 2e-3
+
+
+def test_max_tokens_capped_to_32bit_offsets(capfd):
+    """LAYA_MAX_TOKENS beyond what the kernels' 32-bit buffer offsets reach is capped at load, with a
+    message, and the engine still answers correctly."""
+    d = checkpoint_dir("tiny")
+    b = wl.make_batch(ck.PRESETS["tiny"], [5, 64], [2, 3], seed=3)
+    ref = make_engine(d, "bf16").forward_flat(*b.flat())
+    e = make_engine(d, "bf16", LAYA_MAX_TOKENS=2000000000, LAYA_MAX_GATHERED=2000000000)
+    err = capfd.readouterr().err
+    assert "exceeds what 32-bit buffer offsets reach" in err
+    assert same(e.forward_flat(*b.flat()), ref)

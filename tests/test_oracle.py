@@ -95,6 +95,23 @@ def test_oracle_matches_reference_full_size(tag):
         assert np.abs(got - g[name + "_rows"]).max() < 1e-4, name
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("tag,preset,make", [("c3_full", "large", wl.c3), ("c4_full", "base", wl.c4)])
+def test_oracle_matches_reference_whole_batches(tag, preset, make):
+    """Every question of the b32 x s512 (ModernBERT-large) and b16 x s1024 (mmBERT-base) batches,
+    one question per forward as the engine packs them, against the logits and act logits the
+    reference's fp32 DecisionModel gave on the padded batch (tests/golden/<tag>/drift.npz)."""
+    g = np.load(os.path.join(GOLDEN, tag, "drift.npz"))
+    b = make(0)
+    assert list(g["lens"]) == list(b.lens)
+    cfg = ck.PRESETS[preset]
+    W = om.Weights(ck.generate_weights(cfg, 0))
+    lo, ac = om.run_batch(W, cfg, b)
+    ref = np.concatenate([g["logits"][i, :b.nmark[i]] for i in range(b.B)])
+    assert np.abs(lo - ref).max() < 1e-5
+    assert np.abs(ac.reshape(b.B, -1) - g["act_logits"]).max() < 1e-5
+
+
 # ---------------------------------------------------------------- closed forms and brute force
 def test_zero_weights_give_scorer_bias():
     cfg = ck.PRESETS["tiny"]
