@@ -6,6 +6,11 @@
     layamd_amd/laya-bench       ABI latency tool (p50 per laya_forward_batch call), same (g++)
 
     python -m layamd_amd.build [--jobs N]
+    python -m layamd_amd.build --tile-trace
+
+--tile-trace builds only layamd_amd/liblaya_trace.so, a measurement copy of the library whose GEMM
+kernel records a per-tile timeline (csrc/tile_trace.h; read by python -m layamd_amd.gemm_probe
+--tile-trace).  The product library never contains that code.
 
 Each translation unit is compiled separately (in parallel) into layamd_amd/_build/, then linked.
 HIP code is built with packed-fp32 instruction generation disabled.
@@ -51,6 +56,31 @@ def _newer(target, deps):
     return all(os.path.getmtime(d) <= t for d in deps)
 
 
+TRACE_LIB = os.path.join(PKG, "liblaya_trace.so")
+TRACE_BUILD = os.path.join(PKG, "_build_trace")
+
+
+def build_trace(jobs: int = 8, verbose: bool = True) -> str:
+    """liblaya_trace.so: the HIP sources compiled with -DLAYA_TILE_TRACE (GEMM per-tile timeline)."""
+    os.makedirs(TRACE_BUILD, exist_ok=True)
+    steps = []
+    for s in HIP_SOURCES:
+        src, obj = os.path.join(CSRC, s), os.path.join(TRACE_BUILD, s + ".o")
+        steps.append([HIPCC] + HIP_FLAGS + TU_FLAGS.get(s, []) + ["-DLAYA_TILE_TRACE", "-c", src, "-o", obj])
+    for s in CPP_SOURCES:
+        src, obj = os.path.join(CSRC, s), os.path.join(TRACE_BUILD, s + ".o")
+        steps.append(["g++"] + CXX_FLAGS + ["-c", src, "-o", obj])
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(_run, steps))
+    objs = [st[-1] for st in steps]
+    tmp = TRACE_LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"])
+    os.replace(tmp, TRACE_LIB)
+    if verbose:
+        print("[build] %s" % TRACE_LIB)
+    return TRACE_LIB
+
+
 def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + \
@@ -90,9 +120,13 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--incremental", action="store_true")
+    ap.add_argument("--tile-trace", action="store_true", help="build only the measurement library liblaya_trace.so")
     a = ap.parse_args()
     try:
-        build(a.jobs, force=not a.incremental)
+        if a.tile_trace:
+            build_trace(a.jobs)
+        else:
+            build(a.jobs, force=not a.incremental)
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)

@@ -297,6 +297,44 @@ __device__ __forceinline__ uint32_t pair_rows_to_cols(float ve, float ve1, bool 
 // ======================================================================================
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
+// ---- optional per-tile timeline (built only with -DLAYA_TILE_TRACE: liblaya_trace.so) ----
+// Thread 0 of every workgroup of k_gemm_xl records, at its exit: its start and end on the 100 MHz
+// real-time clock, its prologue, K loop and epilogue in shader-clock cycles, the cycles wave 0 spent
+// in the K loop's stage waits and barriers (two-buffer loop only), and its hardware id.  One record
+// of 8 words per workgroup, at index blockIdx.x, in a device array read back by
+// laya_tile_trace_read (tile_trace.h).
+#ifdef LAYA_TILE_TRACE
+constexpr int kTileTraceMax = 65536;
+__device__ unsigned long long g_tile_trace[8 * kTileTraceMax];
+struct TileTrace {
+  unsigned long long t0, t1, t2, r0, w;
+  __device__ void start() {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+    t1 = t2 = t0;
+    w = 0;
+  }
+  __device__ ~TileTrace() {
+    if (threadIdx.x != 0 || blockIdx.x >= (unsigned)kTileTraceMax) return;
+    const unsigned long long t3 = __builtin_amdgcn_s_memtime(), r3 = __builtin_amdgcn_s_memrealtime();
+    unsigned hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    unsigned long long* p = g_tile_trace + 8 * (size_t)blockIdx.x;
+    p[0] = r0; p[1] = r3; p[2] = t1 - t0; p[3] = t2 - t1; p[4] = t3 - t2; p[5] = w;
+    p[6] = ((unsigned long long)xcc << 32) | hw; p[7] = t3 - t0;
+  }
+};
+#define LAYA_TT_MARK(field) do { if (threadIdx.x == 0) tt.field = __builtin_amdgcn_s_memtime(); } while (0)
+#define LAYA_TT_WAIT_BEGIN const unsigned long long tt_w0_ = __builtin_amdgcn_s_memtime();
+#define LAYA_TT_WAIT_END                                                                          \
+  { const unsigned long long tt_w1_ = __builtin_amdgcn_s_memtime(); __builtin_amdgcn_s_waitcnt(0xC07F); tw += tt_w1_ - tt_w0_; }
+#else
+#define LAYA_TT_MARK(field) do { } while (0)
+#define LAYA_TT_WAIT_BEGIN
+#define LAYA_TT_WAIT_END
+#endif
+
 __device__ __forceinline__ void tile_coords(int bid, int tilesM, int tilesN, int& tm, int& tn) {
   const int p = xcd_remap(bid, tilesM * tilesN);
   constexpr int G = 8;
@@ -437,7 +475,8 @@ __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32
 // reach are issued after the loop.
 template <bool SWAP, int NX, int XP, int XS, int FM, int FN, int PA, int PB, class ST, class XL>
 __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST& T1, const XlDma64<PA, PB>& d, int arow,
-                                            int brow, int hi, int sw, XL&& xl) {
+                                            int brow, int hi, int sw, XL&& xl, unsigned long long& tw) {
+  (void)tw;                                // cycles in stage waits (tile trace builds only)
   constexpr int NMM = FM * FN, E = FM + FN, EW = PB + FM + FN, EA = PA + FM + FN;
   Frags<FM, FN> F0, F1;
   // stage 0; the A part of stage 1 and NX later fills the caller issued may still be in flight
@@ -474,10 +513,12 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
     }                                                                                     \
     LAYA_SUB64(F1, F0, C, 2)                                                              \
     LAYA_SUB64(F0, F1, C, 3)                                                              \
+    LAYA_TT_WAIT_BEGIN                                                                    \
     if constexpr (P >= 0) LAYA_WAIT_VMCNT(XS);                                            \
     else LAYA_WAIT_VMCNT(0);                                                              \
     __builtin_amdgcn_s_barrier();                                                         \
     asm volatile("" ::: "memory");                                                        \
+    LAYA_TT_WAIT_END                                                                      \
     _Pragma("unroll") for (int t = 0; t < NMM; t++) {                                     \
       mma_one_x<SWAP>(acc, F1, t);                                                        \
       _Pragma("unroll") for (int o = t * EA / NMM; o < (t + 1) * EA / NMM; o++) {        \
@@ -696,6 +737,14 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
                 "epilogue LDS");
   static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
 
+#ifdef LAYA_TILE_TRACE
+  TileTrace tt;
+  tt.start();
+  unsigned long long& twait = tt.w;
+#else
+  unsigned long long twait = 0;
+  (void)twait;
+#endif
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
   const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
@@ -896,6 +945,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
 
   const int arow = wm * WTM + l32, brow = wn * WTN + l32;
   const int sw = (lane & 7) ^ ((lane >> 3) & 1);          // g(row) of fragment rows 32 n + lane % 32
+  LAYA_TT_MARK(t1);
 
   if constexpr (RING) {
     if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
@@ -905,14 +955,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     else xl_k_loop64d<false, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
   } else {
     if constexpr (XIN) {
-      if (swap) xl_k_loop64<true, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece);
-      else xl_k_loop64<false, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece);
+      if (swap) xl_k_loop64<true, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, twait);
+      else xl_k_loop64<false, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, twait);
     } else {
       auto none = [](auto) {};
-      if (swap) xl_k_loop64<true, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none);
-      else xl_k_loop64<false, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none);
+      if (swap) xl_k_loop64<true, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, twait);
+      else xl_k_loop64<false, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, twait);
     }
   }
+  LAYA_TT_MARK(t2);
 
   // ---------------- epilogue ----------------
   // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
@@ -1723,3 +1774,17 @@ template void launch_gemm<float>(int, const GemmArgs&, hipStream_t);
 template void launch_gemm<bf16_t>(int, const GemmArgs&, hipStream_t);
 
 }  // namespace laya
+
+#ifdef LAYA_TILE_TRACE
+// the per-tile records of the GEMM launches since the last clear (see TileTrace)
+extern "C" int laya_tile_trace_read(void* host, size_t records) {
+  void* p = nullptr;
+  if (records > (size_t)laya::kTileTraceMax || hipGetSymbolAddress(&p, HIP_SYMBOL(laya::g_tile_trace)) != hipSuccess) return -1;
+  return hipMemcpy(host, p, records * 64, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+extern "C" int laya_tile_trace_clear() {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(laya::g_tile_trace)) != hipSuccess) return -1;
+  return hipMemset(p, 0, sizeof(laya::g_tile_trace)) == hipSuccess ? 0 : -1;
+}
+#endif

@@ -19,6 +19,16 @@ against torch.mm.  Prints a markdown table.
 
 does the same, bf16 only, for the encoder GEMMs of the b32 x s512 ModernBERT-large pass: M = 9664
 rows (the pass's 9514 tokens, packed and padded to 64), (N, K) as above.
+
+    python -m layamd_amd.build --tile-trace && python -m layamd_amd.gemm_probe --tile-trace
+
+loads the measurement library liblaya_trace.so instead and prints, for the pass's encoder GEMM
+shapes (plain store for the QKV and Wi shapes, the fp32 residual update for the two N = 1024 ones)
+on their tile configurations, the per-tile timeline its GEMM records (csrc/tile_trace.h): the
+shader clock the tiles ran at, prologue, K loop, the K loop's stage waits and the epilogue per tile,
+how the tiles' start times spread over the launch, and the K loop's MFMA rate against the rate the
+CU has at that clock (4 SIMDs x 1024 flop per cycle: one v_mfma_f32_32x32x16_bf16 per 32 cycles).
+With --M/--N/--K/--cfg given explicitly it traces that one shape (plain store).
 """
 import argparse
 import time
@@ -96,6 +106,64 @@ def c2(lib, shapes=C2_SHAPES, dtypes=None):
                      t_plan, err), flush=True)
 
 
+# (label, residual epilogue, N, K, tile configuration) at M = 9664: the encoder GEMMs of the
+# b32 x s512 pass on the tiles the tuner picks for them there (and 256x256 for the QKV shape)
+TRACE_C3 = [("QKV shape, store", False, 3072, 1024, 5), ("QKV shape, store", False, 3072, 1024, 0),
+            ("out-proj, residual", True, 1024, 1024, 5), ("Wi shape, store", False, 5248, 1024, 7),
+            ("MLP-out, residual", True, 1024, 2624, 5)]
+# (tile rows, tile columns, workgroups per CU) of the tile configurations
+TILES = {0: (256, 256, 1), 1: (256, 128, 1), 2: (128, 256, 1), 3: (128, 128, 2), 4: (192, 256, 1),
+         5: (160, 256, 1), 6: (128, 192, 2), 7: (192, 128, 2), 8: (128, 64, 2)}
+
+
+def tile_trace(M, cases):
+    import ctypes
+    import numpy as np
+    import torch
+    from layamd_amd import build
+    lib = le.load_library(build.TRACE_LIB)
+    lib.laya_tile_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.laya_tile_trace_read.restype = ctypes.c_int
+    lib.laya_tile_trace_clear.restype = ctypes.c_int
+    g = torch.Generator(device="cpu").manual_seed(0)
+    print("| GEMM (M = %d) | tile | tiles (rounds) | us per launch | span us | clock GHz | prologue us | K loop us "
+          "| stage waits us | epilogue us | K loop MFMA rate at that clock | start spread us (p50, max) |" % M)
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|")
+    for label, resid, N, K, cfg in cases:
+        A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+        W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        C = torch.zeros(M, N, dtype=torch.float32 if resid else torch.bfloat16, device="cuda")
+        le.gemm_config(lib, cfg)
+        for _ in range(3):
+            le.gemm(lib, A, W, C, residual=resid)
+        torch.cuda.synchronize()
+        _spin()
+        per_us = le.gemm(lib, A, W, C, residual=resid, iters=10) / 10 * 1e3
+        torch.cuda.synchronize()
+        assert lib.laya_tile_trace_clear() == 0
+        le.gemm(lib, A, W, C, residual=resid)
+        torch.cuda.synchronize()
+        bm, bn, per_cu = TILES[cfg]
+        nt = ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
+        rec = np.zeros(8 * nt, np.uint64)
+        assert lib.laya_tile_trace_read(rec.ctypes.data, nt) == 0
+        r = rec.reshape(nt, 8).astype(np.float64)
+        assert (r[:, 7] > 0).all(), "a tile left no record"
+        r0, r3 = r[:, 0], r[:, 1]
+        dur_us = (r3 - r0) / 100.0                          # 100 MHz real-time clock
+        ghz = r[:, 7].sum() / dur_us.sum() / 1e3
+        us = lambda col: r[:, col].mean() / ghz / 1e3
+        kloop = us(3)
+        rate = 2.0 * bm * bn * K / (kloop * 1e-6) * per_cu        # flop/s of one CU in the K loop
+        peak = 4 * 1024 * ghz * 1e9
+        start = (r0 - r0.min()) / 100.0
+        print("| %s %dx%dx%d | %dx%d%s | %d (%.2f) | %.1f | %.1f | %.2f | %.2f | %.2f | %.2f (%.0f%%) | %.2f | %.0f%% | %.1f, %.1f |"
+              % (label, M, N, K, bm, bn, ", 2 per CU" if per_cu == 2 else "", nt, nt / (256.0 * per_cu), per_us,
+                 (r3.max() - r0.min()) / 100.0, ghz, us(2), kloop, us(5), 100 * us(5) / kloop, us(4), 100 * rate / peak,
+                 np.percentile(start, 50), start.max()), flush=True)
+    le.gemm_config(lib, -1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--M", type=int, default=16384)
@@ -107,7 +175,14 @@ def main():
     ap.add_argument("--c3", action="store_true", help="time the b32 x s512 pass's encoder GEMM shapes against torch.mm")
     ap.add_argument("--torch", action="store_true",
                     help="after the engine launches, run torch.mm on the same operands as many times")
-    a = ap.parse_args()
+    ap.add_argument("--tile-trace", action="store_true",
+                    help="per-tile timeline from liblaya_trace.so (python -m layamd_amd.build --tile-trace)")
+    a, _ = ap.parse_known_args()
+    if a.tile_trace:
+        import sys
+        explicit = any(x.split("=")[0] in ("--M", "--N", "--K", "--cfg") for x in sys.argv[1:])
+        tile_trace(a.M if explicit else 9664, [("store", False, a.N, a.K, a.cfg)] if explicit else TRACE_C3)
+        return
     lib = le.load_library()
     import torch
     if a.c2:
