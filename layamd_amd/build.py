@@ -8,7 +8,8 @@
     python -m layamd_amd.build [--jobs N]
     python -m layamd_amd.build --tile-trace
 
---tile-trace builds only layamd_amd/liblaya_trace.so, a measurement copy of the library whose GEMM
+--probes builds only layamd_amd/gemm-wave-probe, a standalone GEMM K-loop probe (4 against 8 waves
+per tile).  --tile-trace builds only layamd_amd/liblaya_trace.so, a measurement copy of the library whose GEMM
 kernel records a per-tile timeline (csrc/tile_trace.h; read by python -m layamd_amd.gemm_probe
 --tile-trace).  The product library never contains that code.
 
@@ -81,6 +82,21 @@ def build_trace(jobs: int = 8, verbose: bool = True) -> str:
     return TRACE_LIB
 
 
+PROBES = {"gemm-wave-probe": "gemm_wave_probe.hip"}
+
+
+def build_probes(verbose: bool = True) -> None:
+    """Standalone measurement programs (layamd_amd/<name>), not part of the library."""
+    for exe, src in PROBES.items():
+        out = os.path.join(PKG, exe)
+        _run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Wno-unused-result", "-Wno-unused-value",
+              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-o", out + ".tmp",
+              os.path.join(CSRC, "tools", src)])
+        os.replace(out + ".tmp", out)
+        if verbose:
+            print("[build] %s" % out)
+
+
 def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + \
@@ -121,9 +137,12 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--incremental", action="store_true")
     ap.add_argument("--tile-trace", action="store_true", help="build only the measurement library liblaya_trace.so")
+    ap.add_argument("--probes", action="store_true", help="build only the standalone measurement programs")
     a = ap.parse_args()
     try:
-        if a.tile_trace:
+        if a.probes:
+            build_probes()
+        elif a.tile_trace:
             build_trace(a.jobs)
         else:
             build(a.jobs, force=not a.incremental)
