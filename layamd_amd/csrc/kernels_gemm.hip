@@ -297,6 +297,9 @@ __device__ __forceinline__ uint32_t pair_rows_to_cols(float ve, float ve1, bool 
 // ======================================================================================
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
+// widest power-of-two column count <= cap that divides w
+constexpr int xl_fitw(int w, int cap) { int c = w & -w; while (c > cap) c /= 2; return c; }
+
 // ---- optional per-tile timeline (built only with -DLAYA_TILE_TRACE: liblaya_trace.so) ----
 // Thread 0 of every workgroup of k_gemm_xl records, at its exit: its start and end on the 100 MHz
 // real-time clock, its prologue, K loop and epilogue in shader-clock cycles, the cycles wave 0 spent
@@ -473,9 +476,11 @@ __device__ __forceinline__ void load_frag64(Frags<FM, FN>& f, int idx, const u32
 // leaves those XS loads in flight, vmcnt(XS), and the next stage's wait covers them, so each piece
 // has about a stage and a half to land while the MFMAs run.  Pieces of stages that K does not
 // reach are issued after the loop.
-template <bool SWAP, int NX, int XP, int XS, int FM, int FN, int PA, int PB, class ST, class XL>
+// NT > 0: tail() issues NT vector-memory loads of the caller's (the residual epilogue's first X
+// block) before the last stage's final three sub-steps; the loop's closing wait leaves them in flight.
+template <bool SWAP, int NX, int XP, int XS, int NT, int FM, int FN, int PA, int PB, class ST, class XL, class TL>
 __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST& T1, const XlDma64<PA, PB>& d, int arow,
-                                            int brow, int hi, int sw, XL&& xl, unsigned long long& tw) {
+                                            int brow, int hi, int sw, XL&& xl, TL&& tail, unsigned long long& tw) {
   (void)tw;                                // cycles in stage waits (tile trace builds only)
   constexpr int NMM = FM * FN, E = FM + FN, EW = PB + FM + FN, EA = PA + FM + FN;
   Frags<FM, FN> F0, F1;
@@ -548,6 +553,10 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
   }
   if (g + 2 == nst) LAYA_STAGE64(T0, T1, -1)  // g is even: stage g in T0; the last one is in T1
   ST& L = (g & 1) ? T1 : T0;               // the last stage (g == nst - 1)
+  if constexpr (NT > 0) {
+    tail();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   LAYA_SUB64(F0, F1, L, 1)
   LAYA_SUB64(F1, F0, L, 2)
   LAYA_SUB64(F0, F1, L, 3)
@@ -555,7 +564,7 @@ __device__ __forceinline__ void xl_k_loop64(f32x16_t (&acc)[FM][FN], ST& T0, ST&
   for (int t = 0; t < NMM; t++) mma_one_x<SWAP>(acc, F1, t);
 #undef LAYA_STAGE64
 #undef LAYA_SUB64
-  LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
+  LAYA_WAIT_VMCNT(NT);                     // the refills past the last stage (not the tail's loads)
   if constexpr (XP > 0) {
     static_for<0, XP>([&](auto p) {        // pieces of stages K did not reach
       if (decltype(p)::value >= xdone) xl(p);
@@ -907,12 +916,43 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   // The sum and its order are the same in all three.
   constexpr bool XRES = EPI == EPI_RESID;
   constexpr bool ONE_PER_CU = NST * 16 > 80 * 1024;
-  constexpr bool XIN = XRES && LOOP == 0 && ONE_PER_CU && FM * FN * 16 <= 160;
-  constexpr bool XPRE = XRES && !XIN && FM * FN * 16 <= 64;
-  constexpr bool XEPI = XRES && !XIN && !XPRE;
+  // XFL (every residual kernel but the LayerNorm-fold producers, which need the updated values in
+  // the accumulator layout for their statistics): X is read in the epilogue's flush order, 16 bytes
+  // per lane along each staged row, so one load instruction covers eight whole 128-byte row
+  // segments, and added to the staged product as it is stored.  The accumulator-layout loads of the
+  // other placements touch 32 rows per instruction, 32 bytes of each, and re-request every line four
+  // times; issued during the K loop they slowed it by a quarter.  Each staged block's X is loaded
+  // one block ahead, the first block's during the K loop's last stage.
+  constexpr bool XFL = XRES && !LNX;
+  constexpr bool XIN = XRES && !XFL && LOOP == 0 && ONE_PER_CU && FM * FN * 16 <= 160;
+  constexpr bool XPRE = XRES && !XFL && !XIN && FM * FN * 16 <= 64;
+  constexpr bool XEPI = XRES && !XFL && !XIN && !XPRE;
   f32x4_t xr[XIN || XPRE ? FM : 1][XIN || XPRE ? FN : 1][4];
   const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
       XRES ? a.X : nullptr, (short)0, XRES ? (int)((size_t)a.M * a.ldx * sizeof(float)) : 0, 0x00020000);
+  // XFL: the residual epilogue stages 32 rows x XCW fp32 columns per block (XCPR 16-byte chunks per
+  // row); lane item lane + 64 it of a block is row item / XCPR, chunk item % XCPR
+  constexpr int XCW = xl_fitw(WTN, SB / 128), XCPR = XCW / 4, XNIT = 32 * XCPR / 64, XNB = FM * (WTN / XCW);
+  // XFLK: tiles alone on their CU with the two-buffer loop and room for all of X in registers: the
+  // K loop's first XNB stages each issue one block's loads (piece p = block p), so X is read while
+  // the MFMAs run instead of at the end, where every tile of a one-round launch would read it at
+  // once.  Other XFL tiles load each block one block ahead in the epilogue (the first one during
+  // the K loop's last stage).
+  constexpr bool XFLK = XFL && LOOP == 0 && ONE_PER_CU && XNB * XNIT * 4 <= 160;
+  f32x4_t xall[XFLK ? XNB : 1][XFL ? XNIT : 1];
+  f32x4_t xq[XFL && !XFLK ? 2 : 1][XFL ? XNIT : 1];
+  // X of staged block kb (block row kb / (WTN / XCW), column part kb % (WTN / XCW)) into xv
+  auto xfl_load = [&](f32x4_t (&xv)[XFL ? XNIT : 1], int kb) {
+    if constexpr (XFL) {
+      const int i = kb / (WTN / XCW), c0 = cbase + (kb % (WTN / XCW)) * XCW;
+#pragma unroll
+      for (int it = 0; it < XNIT; it++) {
+        const int item = lane + 64 * it, r = item / XCPR, q = item % XCPR;
+        const uint32_t off = ((uint32_t)(rbase + i * 32 + r) * (uint32_t)a.ldx + (uint32_t)(c0 + 4 * q)) * 4u;
+        xv[it] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
+      }
+    }
+  };
   // X at rows rbase + 32 i + lane % 32, columns cbase + 32 j + 8 g + 4 hi .. + 3
   auto xload = [&](int i, int j, int g) -> f32x4_t {
     const uint32_t off = ((uint32_t)(rbase + i * 32 + l32) * (uint32_t)a.ldx + (uint32_t)(cbase + j * 32 + 8 * g + 4 * hi)) * 4u;
@@ -955,15 +995,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     else xl_k_loop64d<false, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
   } else {
     if constexpr (XIN) {
-      if (swap) xl_k_loop64<true, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, twait);
-      else xl_k_loop64<false, NTX, FM * FN, 4>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, twait);
+      if (swap) xl_k_loop64<true, NTX, FM * FN, 4, 0>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, [] {}, twait);
+      else xl_k_loop64<false, NTX, FM * FN, 4, 0>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, [] {}, twait);
+    } else if constexpr (XFLK) {
+      auto piece = [&](auto p) { xfl_load(xall[decltype(p)::value], decltype(p)::value); };
+      if (swap) xl_k_loop64<true, NTX, XNB, XNIT, 0>(acc, T0, T1, dm, arow, brow, hi, sw, piece, [] {}, twait);
+      else xl_k_loop64<false, NTX, XNB, XNIT, 0>(acc, T0, T1, dm, arow, brow, hi, sw, piece, [] {}, twait);
+    } else if constexpr (XFL) {
+      auto none = [](auto) {};
+      auto first = [&] { xfl_load(xq[0], 0); };
+      if (swap) xl_k_loop64<true, NTX, 0, 0, XNIT>(acc, T0, T1, dm, arow, brow, hi, sw, none, first, twait);
+      else xl_k_loop64<false, NTX, 0, 0, XNIT>(acc, T0, T1, dm, arow, brow, hi, sw, none, first, twait);
     } else {
       auto none = [](auto) {};
-      if (swap) xl_k_loop64<true, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, twait);
-      else xl_k_loop64<false, NTX, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, twait);
+      if (swap) xl_k_loop64<true, NTX, 0, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, [] {}, twait);
+      else xl_k_loop64<false, NTX, 0, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, [] {}, twait);
     }
   }
   LAYA_TT_MARK(t2);
+  if constexpr (XFLK) {
+    // Every X piece has landed by now (issued in the first stages; the loop's own waits, which the
+    // compiler does not see, covered them).  Saying so with a wait it sees keeps it from waiting on
+    // them in the flush, where each such wait would also hold every store issued before it.
+    __builtin_amdgcn_s_waitcnt(0x0F70);                   // vmcnt(0); expcnt, lgkmcnt: no wait
+  }
 
   // ---------------- epilogue ----------------
   // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
@@ -1059,6 +1114,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     float* const xo = EPI == EPI_PARTIAL ? a.X + (size_t)split * a.M * a.ldx : a.X;
     constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
     static_assert(CW % 32 == 0, "whole accumulator blocks per staged block");
+    static_assert(CW == XCW && CPR == XCPR, "XFL block geometry");
+    if constexpr (XFL && LOOP != 0) xfl_load(xq[0], 0);   // (the ring and deep loops have no tail hook)
     float4 bb[FN][4] = {};
 #pragma unroll
     for (int j = 0; j < FN; j++)
@@ -1083,7 +1140,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
     // acc + X of block (i, j), elements 4 g .. 4 g + 3
     auto accx = [&](int i, int j, int g) -> f32x4_t {
       f32x4_t v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-      if constexpr (XRES) {
+      if constexpr (XRES && !XFL) {
         f32x4_t x;
         if constexpr (XEPI) x = xb[i % XB][j][g];
         else x = xr[i][j][g];
@@ -1104,6 +1161,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
       }
 #pragma unroll
       for (int cp = 0; cp < WTN / CW; cp++) {
+        const int kb = i * (WTN / CW) + cp;               // staged block index
+        if constexpr (XFL && !XFLK) {
+          if (kb + 1 < XNB) xfl_load(xq[(kb + 1) & 1], kb + 1);
+        }
 #pragma unroll
         for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++) {
           float v16[16];
@@ -1111,10 +1172,11 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           for (int g = 0; g < 4; g++) {
             const f32x4_t s4 = accx(i, j, g);
             float4 v;
-            v.x = ab(s4[0], bb[j][g].x);
-            v.y = ab(s4[1], bb[j][g].y);
-            v.z = ab(s4[2], bb[j][g].z);
-            v.w = ab(s4[3], bb[j][g].w);
+            // (XFL stages the bare product: X, then the bias, are added in the flush)
+            v.x = XFL ? s4[0] : ab(s4[0], bb[j][g].x);
+            v.y = XFL ? s4[1] : ab(s4[1], bb[j][g].y);
+            v.z = XFL ? s4[2] : ab(s4[2], bb[j][g].z);
+            v.w = XFL ? s4[3] : ab(s4[3], bb[j][g].w);
             *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
             v16[4 * g + 0] = v.x; v16[4 * g + 1] = v.y; v16[4 * g + 2] = v.z; v16[4 * g + 3] = v.w;
           }
@@ -1147,10 +1209,34 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
           }
         }
         const int c0 = cbase + cp * CW;
-        flush(CPR, [&](int r) -> char* {
-          const int m = rbase + i * 32 + r;
-          return m < a.M ? reinterpret_cast<char*>(xo + (size_t)m * a.ldx + c0) : nullptr;
-        }, nchunks(a.N - c0, 4, CPR));
+        if constexpr (XFL) {
+          // (staged + X) + bias, rounded as the other placements round it: X + product, then bias
+          const int nq = nchunks(a.N - c0, 4, CPR);
+          const f32x4_t(&xv)[XNIT] = XFLK ? xall[XFLK ? kb : 0] : xq[XFLK ? 0 : kb & 1];
+          sync_wave();
+#pragma unroll
+          for (int it = 0; it < XNIT; it++) {
+            const int item = lane + 64 * it, r = item / CPR, q = item % CPR;
+            const int m = rbase + i * 32 + r;
+            if (m < a.M && q < nq) {
+              const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + sidx(r, q, CPR));
+              float4 bq = make_float4(0.f, 0.f, 0.f, 0.f);
+              if constexpr (HB) bq = bias4(c0 + 4 * q);
+              f32x4_t o;
+              o[0] = ab(__fadd_rn(sv[0], xv[it][0]), bq.x);
+              o[1] = ab(__fadd_rn(sv[1], xv[it][1]), bq.y);
+              o[2] = ab(__fadd_rn(sv[2], xv[it][2]), bq.z);
+              o[3] = ab(__fadd_rn(sv[3], xv[it][3]), bq.w);
+              *reinterpret_cast<f32x4_t*>(xo + (size_t)m * a.ldx + c0 + 4 * q) = o;
+            }
+          }
+          sync_wave();
+        } else {
+          flush(CPR, [&](int r) -> char* {
+            const int m = rbase + i * 32 + r;
+            return m < a.M ? reinterpret_cast<char*>(xo + (size_t)m * a.ldx + c0) : nullptr;
+          }, nchunks(a.N - c0, 4, CPR));
+        }
         if constexpr (LNP) {
           // the same block again as bf16 (Xh, the next GEMM's A operand)
           constexpr int CPH = CW / 8;
