@@ -85,11 +85,13 @@ int laya_ext_gemm_config(int cfg);
  * shape cannot use) runs as one launch.  Returns 0, or -2 for an invalid value. */
 int laya_ext_gemm_split(int split_rows, int cfg_tail);
 
-/* Split-K factor (0 or 1: none, up to 64) for later bf16 laya_ext_gemm calls, process-wide: K is
- * cut into that many chunks (K must be a multiple of 64 * ks, else the call runs unsplit) whose
- * fp32 partial products go to the caller's device workspace ws (ws_bytes; rows are processed in
- * chunks that fit it) and are summed in chunk order.  The engine uses it for its GEMMs on the
- * gathered head rows and the scorer.  Returns the previous factor, or -2 for an invalid value. */
+/* Split-K factor (0 or 1: none, up to 64) for later bf16 laya_ext_gemm calls, process-wide: K
+ * (at least 128) is cut into chunks of whole 64-deep stages, ceil(K / 64 / ks) stages each (the
+ * last chunk shorter when ks does not divide K / 64; at most ks chunks), whose fp32 partial
+ * products go to the caller's device workspace ws (ws_bytes; rows are processed in chunks that
+ * fit it) and are summed in chunk order.  The engine uses it for its GEMMs on the gathered head
+ * rows and the scorer, and, with LAYA_LATENCY=1, for the residual GEMMs over all rows.  Returns the
+ * previous factor, or -2 for an invalid value. */
 int laya_ext_gemm_ksplit(int ks, void* ws, size_t ws_bytes);
 
 /* laya_ext_gemm's split-K path (bf16 operands, epi 0 store or 1 fp32 residual update, as for

@@ -353,6 +353,7 @@ struct Engine : EngineIface {
     // (4.8 us) and the consumers' per-element fold (+2.6 to +5 us) cost more than the 12.7 us
     // LayerNorm kernels they replace.
     fold_ln = sizeof(T) == 2 && D % 64 == 0 && D <= 2048 && env_int("LAYA_LN_FOLD", 0) != 0;
+    latency = sizeof(T) == 2 && env_int("LAYA_LATENCY", 0) != 0;
     enc.resize(cfg.n_layers);
     for (int i = 0; i < cfg.n_layers; i++) {
       const std::string p = "encoder.layers." + std::to_string(i) + ".";
@@ -584,6 +585,41 @@ struct Engine : EngineIface {
     g.ws = sk_ws;
     g.ws_bytes = kSplitKBytes;
   }
+  // LAYA_LATENCY=1 (bf16, read at laya_create): the residual GEMMs over all rows (the encoder's
+  // out-projection and MLP down-projection, the first head layers' out-projection and FFN
+  // down-projection) also split K, into chunks of kLatencyStages 64-deep stages, whatever the
+  // pass's size.  A pass of a few hundred rows then puts several workgroups on each of the 8-16
+  // tiles these N = 1024 GEMMs have, instead of walking all of K on a few CUs.  The chunking
+  // depends only on K, so every row's result is the same in every batch (and differs from the
+  // default engine's in the last bits: the partial sums are added in chunk order).  Larger
+  // passes pay for the fp32 partials: the mode is for latency-bound serving of small batches.
+  // When a pass's partial products fit the workspace in one piece, the GEMM only writes them and
+  // the LayerNorm that follows adds them to x (in the reduction's order, so the same bits) before
+  // normalising: no reduction launch, and x is read and written once instead of twice.
+  static constexpr int kLatencyStages = 4;
+  bool latency = false;
+  PendingPartials pend;                               // partials the next LayerNorm over all rows adds
+  void splitk_latency(GemmArgs& g) {
+    if (!latency || sizeof(T) != 2 || !sk_ws || g.Xh || g.K % 64) return;
+    const int stages = g.K / 64;
+    if (stages <= kLatencyStages) return;
+    g.ksplit = (stages + kLatencyStages - 1) / kLatencyStages;
+    g.ws = sk_ws;
+    g.ws_bytes = kSplitKBytes;
+    const int ch = gemm_splitk_chunks(g.K, g.ksplit);
+    if (dump_dir.empty() && !fold_ln && (size_t)g.M * ch * g.N * sizeof(float) <= kSplitKBytes) {
+      g.partials_only = true;
+      pend = PendingPartials{sk_ws, ch, (size_t)g.M * g.N, g.bias, g.X};
+    }
+  }
+  // the pending partials for the next LayerNorm (null when none), handed over once
+  const PendingPartials* take_pending() {
+    if (!pend.p) return nullptr;
+    pend_taken = pend;
+    pend = PendingPartials{};
+    return &pend_taken;
+  }
+  PendingPartials pend_taken;
 
   GemmArgs gemm_args(const T* A, int lda, const T* W, int M, int N, int K, const float* bias) {
     GemmArgs g;
@@ -725,6 +761,7 @@ struct Engine : EngineIface {
     auto h2d = [&](void* d, const void* h, size_t n) { LAYA_HIP(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, st)); };
     bind(s);
     h2d(d_blob, h_blob, blob_layout(s).total);
+    pend = PendingPartials{};
 
     // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
 #define STAGE(name, ...) do { if (!collecting) { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
@@ -761,12 +798,13 @@ struct Engine : EngineIface {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
         g.X = x; g.ldx = D;
         if (fold_ln) fold_out(g);
+        splitk_latency(g);
         GSTAGE("enc:gemm_attn_out_res", gemm(EPI_RESID, g, st));
         if (fold_ln) STAGE("enc:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
       }
       if (!fold_ln)
         STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, e.mlp_norm, nullptr, nullptr, nullptr, nullptr,
-                                                   nullptr, xn, st));
+                                                   nullptr, xn, st, nullptr, take_pending()));
       {
         GemmArgs g = gemm_args(xn, D, e.Wi, T_, 2 * I, D, nullptr);
         g.C = mg; g.ldc = I;
@@ -777,6 +815,7 @@ struct Engine : EngineIface {
         GemmArgs g = gemm_args(mg, I, e.Wmo, T_, D, I, nullptr);
         g.X = x; g.ldx = D;
         if (fold_ln && !last_layer) fold_out(g);
+        splitk_latency(g);
         GSTAGE("enc:gemm_mlp_out_res", gemm(EPI_RESID, g, st));
         if (fold_ln && !last_layer)
           STAGE("enc:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
@@ -785,13 +824,15 @@ struct Engine : EngineIface {
       if (!last_layer) {
         if (!fold_ln)
           STAGE("enc:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, enc[L + 1].attn_norm, nullptr, nullptr,
-                                                     nullptr, nullptr, nullptr, xn, st));
+                                                     nullptr, nullptr, nullptr, xn, st, nullptr, take_pending()));
       } else {
         // final_norm then + type_emb[qtype of the row's question] (ref/rl_common.py:104), in place;
         // with the fold also its bf16 copy and statistics, which the head's first GEMM reads
+        const PendingPartials* pp = take_pending();
+        if (pp) pend_taken.xout = nullptr;              // x is overwritten by the normalised rows here
         STAGE("enc:final_ln_type", launch_layernorm<float, T>(x, nullptr, T_, D, eps, final_norm, nullptr, type_emb,
                                                               d_qt, d_seq, x, fold_ln ? xn : (T*)nullptr, st,
-                                                              fold_ln ? ln_mr : nullptr));
+                                                              fold_ln ? ln_mr : nullptr, pp));
       }
     }
     dump("final", x, T_);
@@ -801,7 +842,7 @@ struct Engine : EngineIface {
       const bool last = L == cfg.head_layers - 1;
       if (!fold_ln)
         STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n1w, hl.n1b, nullptr, nullptr, nullptr,
-                                                    nullptr, xn, st));
+                                                    nullptr, xn, st, nullptr, take_pending()));
       {
         GemmArgs g = gemm_args(xn, D, hl.inW, T_, 3 * D, D, hl.inB);
         g.Q = q; g.Kt = k; g.ldqk = D; g.Vt = vt; g.ldv = (int)VTC; g.H = H; g.HD = HD; g.pos = d_pos;
@@ -813,16 +854,18 @@ struct Engine : EngineIface {
                                                d_vlen, nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           if (fold_ln) fold_out(g);
+          splitk_latency(g);
           GSTAGE("head:gemm_out_res", gemm(EPI_RESID, g, st)); }
         if (fold_ln) STAGE("head:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
         if (!fold_ln)
           STAGE("head:ln", launch_layernorm<float, T>(x, nullptr, T_, D, eps, hl.n2w, hl.n2b, nullptr, nullptr, nullptr,
-                                                      nullptr, xn, st));
+                                                      nullptr, xn, st, nullptr, take_pending()));
         { GemmArgs g = gemm_args(xn, D, hl.l1W, T_, FF, D, hl.l1B); g.C = ff; g.ldc = FF; g.act = ACT_RELU;
           if (fold_ln) fold_in(g, hl.c_l1);
           GSTAGE("head:gemm_ffn1_relu", gemm(EPI_STORE, g, st)); }
         { GemmArgs g = gemm_args(ff, FF, hl.l2W, T_, D, FF, hl.l2B); g.X = x; g.ldx = D;
           if (fold_ln) fold_out(g);
+          splitk_latency(g);
           GSTAGE("head:gemm_ffn2_res", gemm(EPI_RESID, g, st)); }
         if (fold_ln) STAGE("head:ln_rowstats", launch_ln_rowstats(ln_stats, (int)MT, D / 64, T_, eps, ln_mr, st));
         if (!dump_dir.empty() && !capturing) { char nm[32]; snprintf(nm, sizeof nm, "head%d", L); dump(nm, x, T_); }

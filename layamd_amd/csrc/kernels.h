@@ -14,10 +14,22 @@ namespace laya {
 // Writes y32 (fp32, may alias x) and/or yT (storage type), and with ymr the mean and rstd (eps) of
 // each output row, ymr[row * 2 + {0, 1}] (what the GEMMs' LayerNorm fold reads, GemmArgs::ln_mr).
 // D % 4 == 0, D <= 2048.
+// A split-K residual GEMM's partial products left for the next LayerNorm to add (see
+// GemmArgs::partials_only): before normalising row r the kernel forms
+//   x' = x + ((p[0][r] + p[1][r] + ... + p[ks - 1][r]) + bias)      (the split-K reduction's order)
+// from slices p[k] = p + k * stride (rows of D floats), writes x' to xout (may alias x) and
+// normalises x'.
+struct PendingPartials {
+  const float* p = nullptr;
+  int ks = 0;
+  size_t stride = 0;
+  const float* bias = nullptr;
+  float* xout = nullptr;
+};
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
                       const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st,
-                      float* ymr = nullptr);
+                      float* ymr = nullptr, const PendingPartials* pend = nullptr);
 
 // The mean and rstd (eps) of each of `rows` rows of width 64 G (G <= 32) from their per-group statistics
 // (GemmArgs::stats layout, ldst rows per group), combined in group order:
@@ -52,13 +64,21 @@ struct GemmArgs {
   // rows [split_rows, M) run as a second launch with configuration cfg_tail (0: one launch); the
   // first launch then covers whole rounds of large tiles and the second the few rows left over
   int split_rows = 0, cfg_tail = -1;
-  // split-K (bf16 EPI_STORE / EPI_RESID): K in ksplit equal chunks whose fp32 partial products go to
-  // the workspace ws (ws_bytes; rows are processed in chunks that fit it) and are summed in chunk
-  // order, then bias, activation or the residual add.  The result of a row depends on ksplit, not
+  // split-K (bf16 EPI_STORE / EPI_RESID): K in ksplit chunks of whole 64-deep stages (equal when
+  // ksplit divides K / 64, else ceil(K / 64 / ksplit) stages each and a shorter last one) whose
+  // fp32 partial products go to the workspace ws (ws_bytes; rows are processed in chunks that fit
+  // it) and are summed in chunk order, then bias, activation or the residual add.  The result of a row depends on ksplit, not
   // on M, so a call site that always passes the same ksplit stays independent of the batch.
   int ksplit = 1;
   float* ws = nullptr;
   size_t ws_bytes = 0;
+  // K chunks of whole 64-deep stages: ceil(stages / ksplit) each, the last one shorter when ksplit
+  // does not divide the stage count (set by the split-K launcher: kfull = the full K, K = a chunk)
+  int kfull = 0;
+  // EPI_RESID split-K whose M rows fit the workspace in one piece: write the partial products
+  // (gemm_splitk_chunks(K, ksplit) slices of M x N floats at ws, slice k at ws + k M N) and leave
+  // their reduction and the residual add to the next LayerNorm (PendingPartials); otherwise ignored
+  bool partials_only = false;
   // LayerNorm folded across two GEMMs (bf16 tiled kernel only; not with split-K).
   //   Producer, EPI_RESID (N % 64 == 0): besides X, writes Xh [M][ldxh] = bf16 of the updated X
   //   and, per row and 64-column group g, the group's sum and its sum of squared deviations from
@@ -92,6 +112,12 @@ void gemm_pin_split(int split_rows, int cfg_tail);
 // returns the previous one
 int gemm_pin_ksplit(int ks);
 constexpr int kGemmConfigs = 9;
+// the number of K chunks a split-K launch with factor ks uses for this K (whole 64-deep stages,
+// ceil(stages / ks) per chunk, empty chunks dropped)
+inline int gemm_splitk_chunks(int K, int ks) {
+  const int stages = K / 64, per = (stages + ks - 1) / ks;
+  return (stages + per - 1) / per;
+}
 // the achievable-MFMA probe: blocks x 4 waves, each iters x 8 MFMAs of 32x32x16 bf16 (32768 flop);
 // out holds blocks x 256 floats
 void launch_mfma_loop(float* out, int blocks, int iters, hipStream_t st);

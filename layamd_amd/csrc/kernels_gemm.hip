@@ -828,7 +828,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
   dm.wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
   dm.lda8 = 8 * lda_b;
   dm.ldw8 = 8 * ldw_b;
-  dm.ns = a.K / 32;
+  // 32-deep slices of this workgroup's K (a split-K chunk: the last one may be shorter)
+  dm.ns = (EPI == EPI_PARTIAL && a.kfull > 0 ? min(a.K, a.kfull - (int)k0) : a.K) / 32;
   Stage64& T0 = *reinterpret_cast<Stage64*>(L);
   Stage64& T1 = *reinterpret_cast<Stage64*>(L + SA + SW);
   if constexpr (LOOP == 2) {
@@ -1774,6 +1775,9 @@ static void launch_reduce(const GemmArgs& a, const float* ws, int ks, int M, voi
 // Split-K over rows chunks that fit the workspace: per chunk one launch of ks x tiles workgroups
 // writing fp32 partials (EPI_PARTIAL), then one reduction.
 static void launch_splitk(int epi, const GemmArgs& a, int ks, hipStream_t st) {
+  // chunks of `per` whole stages; ks drops to the number of non-empty chunks
+  const int stages = a.K / 64, per = (stages + ks - 1) / ks;
+  ks = (stages + per - 1) / per;
   const size_t row_bytes = (size_t)ks * a.N * sizeof(float);
   const int rc = (int)std::min<size_t>((size_t)a.M, a.ws_bytes / row_bytes);
   if (rc < 1) { fprintf(stderr, "[laya] gemm: split-K workspace too small\n"); exit(1); }
@@ -1781,13 +1785,15 @@ static void launch_splitk(int epi, const GemmArgs& a, int ks, hipStream_t st) {
     const int mr = std::min(rc, a.M - r0);
     GemmArgs p = rows_from(a, r0);
     p.M = mr;
-    p.K = a.K / ks;
+    p.K = per * 64;
+    p.kfull = a.K;
     p.bias = nullptr;
     p.act = ACT_NONE;
     p.X = a.ws;
     p.ldx = a.N;
     p.ksplit = ks;
     launch_xl_cfg(EPI_PARTIAL, p, 3, st);                 // 128x128 tiles: the most workgroups
+    if (epi == EPI_RESID && a.partials_only && rc >= a.M) return;    // the next LayerNorm reduces
     if (epi == EPI_RESID) {
       launch_reduce<EPI_RESID, ACT_NONE>(a, a.ws, ks, mr, a.X + (size_t)r0 * a.ldx, a.ldx, st);
     } else {
@@ -1814,7 +1820,7 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     if (xl_usable(epi, a)) {
       const int pinned_ks = ln_fold(a) ? 0 : g_ksplit.load(std::memory_order_relaxed);
       const int ks = a.ksplit > 1 ? a.ksplit : pinned_ks;
-      if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % (ks * 64) == 0 && a.ws != nullptr) {
+      if (ks > 1 && (epi == EPI_STORE || epi == EPI_RESID) && a.K % 64 == 0 && a.K >= 128 && a.ws != nullptr) {
         launch_splitk(epi, a, ks, st);
         return;
       }

@@ -116,6 +116,86 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
   }
 }
 
+// The same LayerNorm for a row whose residual update a split-K GEMM left as partial products
+// (PendingPartials): one workgroup per row, thread t owns 16-byte chunk t of the row (D <= 1024).
+// Each thread issues its chunk's loads of x and of all ks partial slices at once (a small pass's
+// rows are few, so the latency of those loads is what counts), sums the partials in chunk order,
+// adds the bias and then x, exactly as the split-K reduction does, and writes the updated row.
+// The mean and variance are summed in the order of k_layernorm (lane l adds its chunks
+// l, l + 64, ... in turn, then the wave sum), so the normalised row has the bits it would have had
+// after a separate reduction.
+constexpr int kPsMaxSlices = 16;
+template <typename T>
+__global__ __launch_bounds__(256) void k_layernorm_ps(const float* __restrict__ x, int D, float eps,
+                                                      const float* __restrict__ w, const float* __restrict__ b,
+                                                      const float* __restrict__ addtab, const int* __restrict__ qt,
+                                                      const int* __restrict__ seq, float* y32, T* __restrict__ yT,
+                                                      PendingPartials pend) {
+  __shared__ float part[4][64];
+  __shared__ float stat;
+  const int row = blockIdx.x, t = threadIdx.x, lane = t & 63, j = t >> 6;
+  const int nc = D >> 2, nch = (nc + 63) >> 6;
+  const float invd = 1.0f / (float)D;
+  const bool own = t < nc;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (own) {
+    const float* pr = pend.p + (size_t)row * D;
+    float4 pk[kPsMaxSlices];
+#pragma unroll
+    for (int k = 0; k < kPsMaxSlices; k++)
+      if (k < pend.ks) pk[k] = reinterpret_cast<const float4*>(pr + k * pend.stride)[t];
+    v = reinterpret_cast<const float4*>(x + (size_t)row * D)[t];
+    float4 acc = pk[0];
+#pragma unroll
+    for (int k = 1; k < kPsMaxSlices; k++)
+      if (k < pend.ks) { acc.x += pk[k].x; acc.y += pk[k].y; acc.z += pk[k].z; acc.w += pk[k].w; }
+    if (pend.bias) {
+      const float4 bb = reinterpret_cast<const float4*>(pend.bias)[t];
+      acc.x += bb.x; acc.y += bb.y; acc.z += bb.z; acc.w += bb.w;
+    }
+    v.x += acc.x; v.y += acc.y; v.z += acc.z; v.w += acc.w;
+    if (pend.xout) reinterpret_cast<float4*>(pend.xout + (size_t)row * D)[t] = v;
+  }
+  // row sum: chunk sums gathered per lane, added in chunk order, then the wave sum (wave 0)
+  part[j][lane] = own ? (v.x + v.y) + (v.z + v.w) : 0.f;
+  __syncthreads();
+  if (j == 0) {
+    float s = 0.f;
+    for (int q = 0; q < nch; q++)
+      if (lane + 64 * q < nc) s += part[q][lane];
+    const float m = wave_sum(s) * invd;
+    if (lane == 0) stat = m;
+  }
+  __syncthreads();
+  const float mean = stat;
+  float dq = 0.f;
+  if (own) {
+    const float a = v.x - mean, bb = v.y - mean, cc = v.z - mean, d = v.w - mean;
+    dq = (a * a + bb * bb) + (cc * cc + d * d);
+  }
+  __syncthreads();
+  part[j][lane] = dq;
+  __syncthreads();
+  if (j == 0) {
+    float qq = 0.f;
+    for (int q = 0; q < nch; q++)
+      if (lane + 64 * q < nc) qq += part[q][lane];
+    const float inv = rsqrtf(fmaf(wave_sum(qq), invd, eps));
+    if (lane == 0) stat = inv;
+  }
+  __syncthreads();
+  const float inv = stat;
+  if (!own) return;
+  const float* add = addtab ? addtab + (size_t)qt[seq[row]] * D : nullptr;
+  const float4 ww = reinterpret_cast<const float4*>(w)[t];
+  float4 o = make_float4((v.x - mean) * inv * ww.x, (v.y - mean) * inv * ww.y, (v.z - mean) * inv * ww.z,
+                         (v.w - mean) * inv * ww.w);
+  if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[t]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
+  if (add) { const float4 aa = reinterpret_cast<const float4*>(add)[t]; o.x += aa.x; o.y += aa.y; o.z += aa.z; o.w += aa.w; }
+  if (y32) reinterpret_cast<float4*>(y32 + (size_t)row * D)[t] = o;
+  if (yT) St4<T>::at(yT + (size_t)row * D, t, o);
+}
+
 // Two rows per wave for rows up to 1024 wide (about 2400 waves for 9.6k rows, 60 VGPRs: eight
 // waves per SIMD, so all of them are resident at once).  In the pass a LayerNorm starts cold after
 // a GEMM; one row per wave (twice the wave launches) or weights held in registers across the
@@ -123,12 +203,25 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
 template <typename Tin, typename T>
 void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float eps, const float* w, const float* b,
                       const float* addtab, const int* qt, const int* seq, float* y32, T* yT, hipStream_t st,
-                      float* ymr) {
+                      float* ymr, const PendingPartials* pend) {
   if (D % 4 || D > kLnMaxChunks * 256) {
     fprintf(stderr, "[laya] layernorm: unsupported width %d\n", D);
     exit(1);
   }
+  const bool ps = pend && pend->p && pend->ks > 0;
+  if (ps && (!std::is_same<Tin, float>::value || gather || ymr || D > 1024 || pend->ks > kPsMaxSlices ||
+             pend->stride < (size_t)rows * D)) {
+    fprintf(stderr, "[laya] layernorm: pending split-K partials need fp32 rows up to 1024 wide, at most %d slices, "
+                    "no gather, no statistics\n", kPsMaxSlices);
+    exit(1);
+  }
   if (rows <= 0) return;
+  if (ps) {
+    if constexpr (std::is_same<Tin, float>::value)
+      LAYA_LAUNCH((k_layernorm_ps<T>), dim3(rows), dim3(64 * ((D / 4 + 63) / 64)), 0, st, x, D, eps, w, b, addtab, qt,
+                  seq, y32, yT, *pend);
+    return;
+  }
   auto go = [&](auto mr) {
     constexpr bool MR = decltype(mr)::value;
     if (D <= 1024) {
@@ -145,11 +238,14 @@ void launch_layernorm(const Tin* x, const int* gather, int rows, int D, float ep
 }
 
 template void launch_layernorm<float, float>(const float*, const int*, int, int, float, const float*, const float*,
-                                             const float*, const int*, const int*, float*, float*, hipStream_t, float*);
+                                             const float*, const int*, const int*, float*, float*, hipStream_t, float*,
+                                             const PendingPartials*);
 template void launch_layernorm<float, bf16_t>(const float*, const int*, int, int, float, const float*, const float*,
-                                              const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*);
+                                              const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*,
+                                              const PendingPartials*);
 template void launch_layernorm<bf16_t, bf16_t>(const bf16_t*, const int*, int, int, float, const float*, const float*,
-                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*);
+                                               const float*, const int*, const int*, float*, bf16_t*, hipStream_t, float*,
+                                               const PendingPartials*);
 
 // One thread per row: the G group pairs (sum, M2) of the row are read group-major (a group's rows
 // are contiguous, so a wave's reads of one group are coalesced), all at once for up to 16 groups,

@@ -31,7 +31,7 @@ EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay",
 # of laya_create only
 ENV_KNOBS = ["LAYA_PRECISION", "LAYA_MAX_TOKENS", "LAYA_PASS_TOKENS", "LAYA_MAX_SEQS", "LAYA_MAX_GATHERED",
              "LAYA_ATTN_QTILE", "LAYA_GRAPHS", "LAYA_MAX_GRAPHS", "LAYA_TUNE", "LAYA_GEMM_CFG", "LAYA_GEMM_SPLIT",
-             "LAYA_PROFILE", "LAYA_DUMP_DIR", "LAYA_VERBOSE", "LAYA_LN_FOLD"]
+             "LAYA_PROFILE", "LAYA_DUMP_DIR", "LAYA_VERBOSE", "LAYA_LN_FOLD", "LAYA_LATENCY"]
 
 _IP = ctypes.POINTER(ctypes.c_int)
 _FP = ctypes.POINTER(ctypes.c_float)

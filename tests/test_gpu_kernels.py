@@ -84,6 +84,40 @@ def test_gemm_encoder_shapes(dtype, M, K, N):
     assert np.all(c_err <= c_tol), (float(c_err.max()), float((c_err / c_tol).max()))
 
 
+@pytest.mark.parametrize("M,K,N,ks", [(512, 1024, 1024, 3), (160, 2624, 1024, 7), (160, 2624, 1024, 11),
+                                       (512, 4096, 1024, 16), (512, 1024, 3072, 4)])
+def test_gemm_split_k_chunks(M, K, N, ks):
+    """bf16 split-K (laya_ext_gemm_ksplit): K in chunks of ceil(K / 64 / ks) whole 64-deep stages,
+    the last one shorter when ks does not divide the stage count (K = 1024 in 3 chunks of 6, 6 and
+    4 stages; K = 2624, 41 stages, in 7 chunks of 6 and one of 5, or 11 of 4 and one of 1), partial
+    products summed in chunk order: the store and the fp32 residual update against an fp64 product
+    with the same bound as the unsplit GEMM (a chunk dropped or read twice is off by O(|C|))."""
+    import torch
+    lib = le.load_library()
+    ws = torch.empty(16 << 20, dtype=torch.float32, device="cuda")
+    prev = le.gemm_ksplit(lib, ks, ws)
+    try:
+        gen = torch.Generator(device="cuda").manual_seed(M + 3 * N + K + ks)
+        A = torch.randn(M, K, generator=gen, device="cuda").to(torch.bfloat16)
+        W = (torch.randn(N, K, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        X0 = torch.randn(M, N, generator=gen, device="cuda")
+        C = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        le.gemm(lib, A, W, C)
+        X = X0.clone()
+        le.gemm(lib, A, W, X, residual=True)
+        torch.cuda.synchronize()
+    finally:
+        le.gemm_ksplit(lib, prev)
+    a, w = A.double().cpu().numpy(), W.double().cpu().numpy()
+    ref = a @ w.T
+    acc_tol = 8 * U32 * np.sqrt(K) * (np.abs(a) @ np.abs(w).T)
+    xn = X.double().cpu().numpy()
+    x_err = np.abs(xn - X0.double().cpu().numpy() - ref)
+    assert np.all(x_err <= acc_tol + U32 * np.abs(xn) + 1e-7), float(x_err.max())
+    c_err = np.abs(C.double().cpu().numpy() - ref)
+    assert np.all(c_err <= acc_tol + 2.0 ** -8 * np.abs(ref) + 1e-7), float(c_err.max())
+
+
 # ---------------------------------------------------------------- attention kernels
 def _up(x, a):
     return (int(x) + a - 1) // a * a

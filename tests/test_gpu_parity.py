@@ -51,7 +51,8 @@ BF16_PROB = 1e-3
 # for laya_create only, so nothing leaks from one engine to the next)
 ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
        "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
-       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None}
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None,
+       "LAYA_LATENCY": None}
 _ENGINES = {}
 
 

@@ -30,7 +30,8 @@ pytestmark = pytest.mark.gpu
 
 ENV = {"LAYA_MAX_TOKENS": 8192, "LAYA_DUMP_DIR": None, "LAYA_PROFILE": None, "LAYA_GRAPHS": 1, "LAYA_TUNE": 1,
        "LAYA_ATTN_QTILE": None, "LAYA_GEMM_CFG": None, "LAYA_GEMM_SPLIT": None, "LAYA_MAX_GRAPHS": None,
-       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None}
+       "LAYA_PASS_TOKENS": None, "LAYA_MAX_SEQS": None, "LAYA_MAX_GATHERED": None, "LAYA_LN_FOLD": None,
+       "LAYA_LATENCY": None}
 
 
 def make_engine(model_dir, precision, **env):
@@ -290,3 +291,57 @@ def test_max_tokens_capped_to_32bit_offsets(capfd):
     err = capfd.readouterr().err
     assert "exceeds what 32-bit buffer offsets reach" in err
     assert same(e.forward_flat(*b.flat()), ref)
+
+
+def test_latency_mode_split_k():
+    """LAYA_LATENCY=1 (bf16): the residual GEMMs over all rows split K into chunks of 4 stages of 64
+    (encoder out-projection K = 1024: 4 chunks; MLP down-projection K = 2624: 10 chunks of 4 stages
+    and one of 1; the first head layer's FFN down-projection K = 4096: 16), whatever the pass's size.
+      * ModernBERT-large b1 x s128: logits and act logits within the bf16 budget of the reference's
+        fp32 model (tests/golden/large), as the default engine;
+      * a question's bits do not depend on its batch: alone, and as the third of four questions,
+        it gives the same logits and act logits; graph replays give the eager pass's bits; the
+        LayerNorm that adds a split GEMM's partial products (when they fit the workspace) gives
+        the bits of the GEMM's own reduction;
+      * pass times (device, graph replay) with and without the mode at 1 x 128, 1 x 512 and
+        4 x 512 tokens are printed."""
+    import json
+    g = np.load(os.path.join(GOLDEN, "large", "golden.npz"))
+    d = checkpoint_dir("large")
+    lat = make_engine(d, "bf16", LAYA_LATENCY=1)
+    eager = make_engine(d, "bf16", LAYA_LATENCY=1, LAYA_GRAPHS=0)
+    b = wl.c1(0)
+    lens, ids, nm, mk, qt = b.flat()
+    lo, ac = lat.forward_flat(lens, ids, nm, mk, qt)
+    gl, g16 = g["logits"][0, :nm[0]], g["logits_bf16_autocast"][0, :nm[0]]
+    dl, dl_up = float(np.abs(lo - gl).max()), float(np.abs(g16 - gl).max())
+    da, da_up = float(np.abs(ac - g["act_logits"]).max()), float(np.abs(g["act_logits_bf16_autocast"] - g["act_logits"]).max())
+    print("latency mode, large c1: dlogit %.5f (reference bf16 %.5f), dact %.5f (reference bf16 %.5f)" % (dl, dl_up, da, da_up))
+    assert dl <= 2.0 * dl_up + 1e-3 and da <= 2.0 * da_up + 1e-3
+    default = make_engine(d, "bf16").forward_flat(lens, ids, nm, mk, qt)
+    print("latency vs default engine: max|dlogit| %.2e" % np.abs(lo - default[0]).max())
+    # batch independence and graph replay
+    cfg = ck.PRESETS["large"]
+    four = wl.make_batch(cfg, [512, 77, 128, 300], [4, 3, 4, 5], seed=21)
+    one = four.subset([2])
+    lo4, ac4 = lat.forward_flat(*four.flat())
+    lo1, ac1 = lat.forward_flat(*one.flat())
+    moff = np.concatenate([[0], np.cumsum(four.nmark)])
+    assert np.array_equal(lo4[moff[2]:moff[3]], lo1) and np.array_equal(ac4.reshape(4, -1)[2], ac1.reshape(-1))
+    assert same(lat.forward_flat(*four.flat()), (lo4, ac4))
+    assert same(eager.forward_flat(*four.flat()), (lo4, ac4))
+    # the partial products are added by the LayerNorm that follows each split GEMM; with per-layer
+    # dumps the GEMMs reduce them themselves (so that the dumped x is whole): the same bits
+    import tempfile
+    with tempfile.TemporaryDirectory() as dd:
+        assert same(make_engine(d, "bf16", LAYA_LATENCY=1, LAYA_DUMP_DIR=dd).forward_flat(*four.flat()), (lo4, ac4))
+    assert np.isfinite(lo4).all() and np.isfinite(ac4).all()
+    # pass times, device-side graph replays
+    times = {}
+    for tag, e in (("default", make_engine(d, "bf16")), ("latency", lat)):
+        for shape in ((1, 128), (1, 512), (4, 512)):
+            bb = wl.make_batch(cfg, [shape[1]] * shape[0], [4] * shape[0], seed=5)
+            e.forward_flat(*bb.flat())
+            e.forward_flat(*bb.flat())
+            times[(tag, shape)] = e.replay(20) / 20
+    print("pass ms (graph replay):", json.dumps({"%s %dx%d" % (t, s[0], s[1]): round(v, 3) for (t, s), v in times.items()}))
