@@ -92,7 +92,7 @@ def stage_work(name, cfg, T, R, KT, B, elt, attn_flops):
         "enc:gemm_mlp_out_res": g(T, D, I),
         "head:gemm_qkv": g(T, 3 * D, D),
         "scorer:gemm_gelu": g(KT, D, D),
-        "enc:embed_ln": (0.0, float(T * D * (elt + 4 + elt))),
+        "enc:embed_ln": (0.0, float(T * D * (4 + 4 + elt))),
         "enc:ln": (0.0, float(T * D * (4 + elt))),
         "enc:final_ln_type": (0.0, float(T * D * 8)),
         "enc:attn_sliding": (attn_flops["sliding"], float(T * D * 4 * elt)),

@@ -145,7 +145,7 @@ struct Engine : EngineIface {
   std::string dump_dir;                       // LAYA_DUMP_DIR at laya_create (empty: no dumps)
 
   // weights
-  T* tok_emb = nullptr;
+  float* tok_emb = nullptr;            // fp32 in both engines, as the reference's embedding output is
   float *emb_norm = nullptr, *final_norm = nullptr, *type_emb = nullptr;
   std::vector<EncLayer> enc;
   std::vector<HeadLayer> head;
@@ -341,7 +341,11 @@ struct Engine : EngineIface {
     SafeTensors st;
     if (!st.open(dir + "/model.safetensors", &err)) { fprintf(stderr, "[laya] %s\n", err.c_str()); exit(1); }
 
-    tok_emb = up_mat(st, "encoder.embeddings.tok_embeddings.weight", V, D);
+    // The token embeddings stay fp32 in the bf16 engine too (0.2 GB for the large model's 50k-token
+    // vocabulary, 0.8 GB for the 256k one): the embedding LayerNorm reads only the pass's rows, and
+    // its output, the start of the fp32 residual stream, then carries no bf16 rounding, as in the
+    // reference's bf16 autocast, where the embedding and its LayerNorm run in fp32.
+    tok_emb = up_f32(st, "encoder.embeddings.tok_embeddings.weight", {V, D});
     emb_norm = up_f32(st, "encoder.embeddings.norm.weight", {D});
     final_norm = up_f32(st, "encoder.final_norm.weight", {D});
     type_emb = up_f32(st, "type_emb.weight", {3, D});
@@ -766,7 +770,7 @@ struct Engine : EngineIface {
     // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
 #define STAGE(name, ...) do { if (!collecting) { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
 #define GSTAGE(name, ...) do { if (collecting) { __VA_ARGS__; } else { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
-    STAGE("enc:embed_ln", launch_layernorm<T, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
+    STAGE("enc:embed_ln", launch_layernorm<float, T>(tok_emb, d_ids, T_, D, eps, emb_norm, nullptr, nullptr, nullptr,
                                                  nullptr, x, enc[0].attn_norm ? nullptr : xn, st));
     dump("emb", x, T_);
     // LayerNorm fold (bf16): a residual GEMM leaves x, its bf16 copy in xn and each row's mean and rstd;
