@@ -268,6 +268,30 @@ __device__ __forceinline__ u32x4_t attn_rsrc(const void* p, uint32_t bytes) {
   return r;
 }
 
+// Optional per-workgroup timeline (-DLAYA_TILE_TRACE, liblaya_trace.so only): thread 0 records at
+// exit, at index blockIdx.y * gridDim.x + blockIdx.x: start and end on the 100 MHz real-time clock,
+// shader cycles from entry to exit, key blocks processed, tile index and head, and its hardware id.
+#ifdef LAYA_TILE_TRACE
+constexpr int kAttnTraceMax = 65536;
+__device__ unsigned long long g_attn_trace[8 * kAttnTraceMax];
+struct AttnTrace {
+  unsigned long long t0, r0;
+  int blocks = 0;
+  __device__ AttnTrace() : t0(__builtin_amdgcn_s_memtime()), r0(__builtin_amdgcn_s_memrealtime()) {}
+  __device__ ~AttnTrace() {
+    const unsigned idx = blockIdx.y * gridDim.x + blockIdx.x;
+    if (threadIdx.x != 0 || idx >= (unsigned)kAttnTraceMax) return;
+    const unsigned long long t3 = __builtin_amdgcn_s_memtime(), r3 = __builtin_amdgcn_s_memrealtime();
+    unsigned hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    unsigned long long* p = g_attn_trace + 8 * (size_t)idx;
+    p[0] = r0; p[1] = r3; p[2] = t3 - t0; p[3] = (unsigned)blocks; p[4] = blockIdx.y; p[5] = blockIdx.x;
+    p[6] = ((unsigned long long)xcc << 32) | hw; p[7] = 1;
+  }
+};
+#endif
+
 template <int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
                                                         int ldqk, int kv_rows, const bf16_t* __restrict__ Vt, int ldv,
@@ -287,6 +311,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   // three four-wave workgroups on a CU.
   __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs[64 * 8];
 
+#ifdef LAYA_TILE_TRACE
+  AttnTrace at;
+#endif
   // heads are the fastest grid dimension, so the (longest-first) tiles start in order
   const AttnTile tile = tiles[blockIdx.y];
   if (tile.nq <= 0) return;                               // an empty tile of the pass's tile capacity
@@ -472,6 +499,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     if (more) fetch_v(k0 + 64);
     k0 += 64;
     ++it;
+#ifdef LAYA_TILE_TRACE
+    at.blocks = it;
+#endif
   };
   if (window_half > 0 && !gq) {
     // sliding window: a tile's few blocks are mostly partly visible; all take the mask
@@ -531,3 +561,17 @@ template void launch_attention<bf16_t>(const bf16_t*, const bf16_t*, int, int, c
                                        int, float, hipStream_t);
 
 }  // namespace laya
+
+#ifdef LAYA_TILE_TRACE
+// the per-workgroup records of the bf16 attention launches since the last clear
+extern "C" int laya_attn_trace_read(void* host, size_t records) {
+  void* p = nullptr;
+  if (records > (size_t)laya::kAttnTraceMax || hipGetSymbolAddress(&p, HIP_SYMBOL(laya::g_attn_trace)) != hipSuccess) return -1;
+  return hipMemcpy(host, p, records * 64, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+extern "C" int laya_attn_trace_clear() {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(laya::g_attn_trace)) != hipSuccess) return -1;
+  return hipMemset(p, 0, sizeof(laya::g_attn_trace)) == hipSuccess ? 0 : -1;
+}
+#endif

@@ -22,6 +22,13 @@ extern "C" {
 int laya_tile_trace_read(void* host, size_t records);
 /* zeroes every record; 0 or -1 */
 int laya_tile_trace_clear(void);
+
+/* The bf16 attention kernel (k_attention_bf16) keeps its own records, one per workgroup at index
+ * blockIdx.y * gridDim.x + blockIdx.x (tile-major, heads fastest), 8 uint64 each:
+ *   [0] start, [1] end (100 MHz real-time clock), [2] shader cycles entry to exit,
+ *   [3] 64-key blocks processed, [4] tile index, [5] head, [6] XCC id << 32 | HW_ID, [7] 1. */
+int laya_attn_trace_read(void* host, size_t records);
+int laya_attn_trace_clear(void);
 #ifdef __cplusplus
 }
 #endif
