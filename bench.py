@@ -191,6 +191,9 @@ def main():
     ap.add_argument("--config", default="c3", choices=["c3", "c4", "c5", "c1"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--stage-sequence", default=None, metavar="FILE",
+                    help="write the stage of every kernel launch of one pass, in launch order (to read a kernel "
+                         "trace of the same run per stage: python -m layamd_amd.trace_table)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one plain copy of 256 MiB (the counter calibration), then "
                          "three forward passes without graphs, then exit")
@@ -265,6 +268,9 @@ def main():
     for _ in range(n_prof):
         eng.forward_flat(*flat)
     stages = eng.prof_stages()
+    if a.stage_sequence:
+        with open(a.stage_sequence, "w") as f:
+            f.write("\n".join(eng.prof_sequence()) + "\n")
     eng.prof_enable(False)
     eng.prof_report(n_prof)
     sys.stdout.flush()

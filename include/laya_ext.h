@@ -19,6 +19,13 @@ int laya_ext_prof_enable(void* h, int on);
  * device milliseconds and number of launches.  Returns 0, or -1 when i is out of range. */
 int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, long long* calls);
 
+/* The stage of every kernel launch of the most recent profiled pass, in launch order: stage
+ * indices as laya_ext_prof_stage numbers them, the first cap of them into stages.  Returns the
+ * number of launches (0 when no pass ran with profiling on), or -1 for invalid arguments.  Lets a
+ * kernel trace of the same pass (graph replays launch the same kernels in the same order) be read
+ * per stage. */
+int laya_ext_prof_sequence(void* h, int* stages, int cap);
+
 /* Re-runs the most recent pass `iters` times exactly as laya_forward_batch runs it (graph replay
  * when graphs are on) and stores the device time of all iterations, measured with HIP events on
  * the engine's stream, in *ms.  Inputs stay resident; only the pass's small index arrays are

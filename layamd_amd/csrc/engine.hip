@@ -58,6 +58,7 @@ struct Prof : LaunchTimer {
   std::vector<std::tuple<std::string, double, long long>> acc;   // stage, ms, stage executions
   std::vector<std::pair<hipEvent_t, hipEvent_t>> pool;
   std::vector<std::pair<size_t, size_t>> pending;                  // (acc index, pool index)
+  std::vector<int> seq;                                            // stage of each launch of the last pass
   size_t cur = 0;
   void init() {
     const char* p = getenv("LAYA_PROFILE");
@@ -72,6 +73,7 @@ struct Prof : LaunchTimer {
       pool.emplace_back(x, y);
     }
     pending.emplace_back(cur, i);
+    seq.push_back((int)cur);
     *a = pool[i].first;
     *b = pool[i].second;
   }
@@ -766,6 +768,7 @@ struct Engine : EngineIface {
     bind(s);
     h2d(d_blob, h_blob, blob_layout(s).total);
     pend = PendingPartials{};
+    if (prof.on && !collecting) prof.seq.clear();
 
     // while the pass is only being listed for tuning, GEMMs are recorded and nothing else runs
 #define STAGE(name, ...) do { if (!collecting) { prof.begin(name); __VA_ARGS__; prof.end(); } } while (0)
@@ -1033,6 +1036,12 @@ int laya_ext_prof_stage(void* h, int i, char* name, int name_len, double* ms, lo
   return 0;
 }
 int laya_ext_replay(void* h, int iters, float* ms) { return E(h)->replay(iters, ms); }
+int laya_ext_prof_sequence(void* h, int* stages, int cap) {
+  if (!h || cap < 0 || (cap > 0 && !stages)) return -1;
+  const auto& q = E(h)->prof.seq;
+  for (int i = 0; i < cap && i < (int)q.size(); i++) stages[i] = q[i];
+  return (int)q.size();
+}
 static float* g_ext_ws = nullptr;          // split-K workspace of laya_ext_gemm (caller's memory)
 static size_t g_ext_ws_bytes = 0;
 

@@ -26,7 +26,8 @@ ABI_SYMBOLS = ["laya_create", "laya_forward_batch", "laya_forward", "laya_n_act"
                "laya_max_markers", "laya_temperature", "laya_prof_report", "laya_prof_reset", "laya_tune_all"]
 EXT_SYMBOLS = ["laya_ext_prof_enable", "laya_ext_prof_stage", "laya_ext_replay", "laya_ext_precision", "laya_ext_gemm",
                "laya_ext_gemm_config", "laya_ext_gemm_split", "laya_ext_gemm_ksplit", "laya_ext_mfma_loop",
-               "laya_ext_stats", "laya_ext_attention", "laya_ext_gemm_splitk_static", "laya_ext_hbm_copy"]
+               "laya_ext_stats", "laya_ext_attention", "laya_ext_gemm_splitk_static", "laya_ext_hbm_copy",
+               "laya_ext_prof_sequence"]
 # every environment variable laya_create reads; Engine() sets the ones it is given for the duration
 # of laya_create only
 ENV_KNOBS = ["LAYA_PRECISION", "LAYA_MAX_TOKENS", "LAYA_PASS_TOKENS", "LAYA_MAX_SEQS", "LAYA_MAX_GATHERED",
@@ -76,6 +77,8 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
     L.laya_ext_prof_stage.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_int,
                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_longlong)]
     L.laya_ext_prof_stage.restype = ctypes.c_int
+    L.laya_ext_prof_sequence.argtypes = [ctypes.c_void_p, _IP, ctypes.c_int]
+    L.laya_ext_prof_sequence.restype = ctypes.c_int
     L.laya_ext_replay.argtypes = [ctypes.c_void_p, ctypes.c_int, _FP]
     L.laya_ext_replay.restype = ctypes.c_int
     L.laya_ext_precision.argtypes = [ctypes.c_void_p]
@@ -326,6 +329,14 @@ class Engine:
             out[name.value.decode()] = (ms.value, calls.value)
             i += 1
         return out
+
+    def prof_sequence(self):
+        """Stage name of every kernel launch of the last profiled pass, in launch order."""
+        names = list(self.prof_stages())
+        n = self.lib.laya_ext_prof_sequence(self.h, None, 0)
+        buf = (ctypes.c_int * max(n, 1))()
+        self.lib.laya_ext_prof_sequence(self.h, buf, n)
+        return [names[buf[i]] for i in range(n)]
 
     def stats(self):
         """(graphs cached, graphs captured, tuned GEMM plans, tuned pass buckets)."""
