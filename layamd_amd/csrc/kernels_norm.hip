@@ -60,6 +60,15 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
       if (c < nc) v[q][j] = Ld4<Tin>::at(xr, c);
     }
   }
+  // the weight, loaded once per wave for its rows, right behind the rows themselves: loaded per row
+  // after the reductions, each row waited for its own round trip to L2 (11.6 -> 10.45 us per launch
+  // at 9664 x 1024)
+  float4 wv[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; j++) {
+    const int c = lane + 64 * j;
+    if (c < nc) wv[j] = reinterpret_cast<const float4*>(w)[c];
+  }
 #pragma unroll
   for (int q = 0; q < RPW; q++)
 #pragma unroll
@@ -86,7 +95,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const Tin* x, const int* __re
     for (int j = 0; j < NCH; j++) {
       const int c = lane + 64 * j;
       if (c < nc) {
-        const float4 ww = reinterpret_cast<const float4*>(w)[c];
+        const float4 ww = wv[j];
         float4 o = make_float4((v[q][j].x - mean) * inv * ww.x, (v[q][j].y - mean) * inv * ww.y,
                                (v[q][j].z - mean) * inv * ww.z, (v[q][j].w - mean) * inv * ww.w);
         if (b) { const float4 bb = reinterpret_cast<const float4*>(b)[c]; o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w; }
