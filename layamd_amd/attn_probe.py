@@ -8,7 +8,11 @@ csrc/tile_trace.h) and runs the encoder's sliding-window (+-64) and global atten
 random bf16 Q, K, V^T packed as the engine packs the batch's questions (16 heads of 64; tiles of
 <= qtile queries, longest questions first, then the bucket's empty tiles).  Prints per launch: the
 device time (mean of 10 launches), the span of the traced launch, the clock, how many workgroups
-were resident at once at most, the mean workgroup time per count of key blocks, how busy the
+were resident at once at most, the mean workgroup time per count of key blocks (and how much of it
+came before the first block: the tile's lookups (tile, then its question's offset and length),
+Q and the first K and V^T block; and how much
+wave 0 spent in the key loop's two waits: V^T landed before the PV step, and the next K landed at
+the end of the block, each with its barrier), how busy the
 resident slots were over the span (sum of workgroup times / (span x the most resident at once)),
 and when the last workgroups started.
 """
@@ -83,8 +87,8 @@ def main():
         n = nt * H
         rec = np.zeros(8 * n, np.uint64)
         assert lib.laya_attn_trace_read(rec.ctypes.data, n) == 0
-        r = rec.reshape(n, 8).astype(np.float64)
-        r = r[r[:, 3] > 0]                                    # workgroups of non-empty tiles
+        r_keep = rec.reshape(n, 8)[:, 3] > 0                  # workgroups of non-empty tiles
+        r = rec.reshape(n, 8)[r_keep].astype(np.float64)
         r0, r3 = r[:, 0], r[:, 1]
         dur = (r3 - r0) / 100.0
         ghz = r[:, 2].sum() / dur.sum() / 1e3
@@ -98,10 +102,18 @@ def main():
         print("%-13s %6.1f us per launch | span %.1f us, clock %.2f GHz, %d workgroups, at most %d resident, "
               "slots busy %.0f%%, last start at %.1f us" % (name, per, span, ghz, len(r), peak, 100 * busy,
                                                             (r0.max() - t0) / 100.0))
+        w7 = rec.reshape(n, 8)[r_keep, 7]
+        pro = (w7 & np.uint64(0xFFFFFFFF)).astype(np.float64) / ghz / 1e3   # entry to the first key block
+        pra = (w7 >> np.uint64(32)).astype(np.float64) / ghz / 1e3          # entry to the tile's lookups done
+        w5 = rec.reshape(n, 8)[r_keep, 5]
+        wv = (w5 >> np.uint64(32)).astype(np.float64) / ghz / 1e3
+        wk = (w5 & np.uint64(0xFFFFFFFF)).astype(np.float64) / ghz / 1e3
         for nb in sorted(set(r[:, 3].astype(int))):
             m = r[:, 3] == nb
-            print("    %d key blocks: %4d workgroups, %.2f us each (p10 %.2f, p90 %.2f)"
-                  % (nb, m.sum(), dur[m].mean(), np.percentile(dur[m], 10), np.percentile(dur[m], 90)))
+            print("    %d key blocks: %4d workgroups, %.2f us each (p10 %.2f, p90 %.2f): %.2f us before the first "
+                  "block (%.2f to the tile's lookups), %.2f us in V^T waits, %.2f us in end-of-block waits"
+                  % (nb, m.sum(), dur[m].mean(), np.percentile(dur[m], 10), np.percentile(dur[m], 90),
+                     pro[m].mean(), pra[m].mean(), wv[m].mean(), wk[m].mean()))
 
 
 if __name__ == "__main__":

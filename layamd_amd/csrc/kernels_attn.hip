@@ -270,13 +270,18 @@ __device__ __forceinline__ u32x4_t attn_rsrc(const void* p, uint32_t bytes) {
 
 // Optional per-workgroup timeline (-DLAYA_TILE_TRACE, liblaya_trace.so only): thread 0 records at
 // exit, at index blockIdx.y * gridDim.x + blockIdx.x: start and end on the 100 MHz real-time clock,
-// shader cycles from entry to exit, key blocks processed, tile index and head, and its hardware id.
+// shader cycles from entry to exit, key blocks processed, tile index and head, the cycles wave 0
+// spent in the two waits of the key loop, its hardware id and the cycles before the first block.
 #ifdef LAYA_TILE_TRACE
 constexpr int kAttnTraceMax = 65536;
 __device__ unsigned long long g_attn_trace[8 * kAttnTraceMax];
 struct AttnTrace {
-  unsigned long long t0, r0;
+  unsigned long long t0, r0, ta = 0, t1 = 0, wv = 0, wk = 0, tw = 0;
   int blocks = 0;
+  __device__ void wait_begin() { if (threadIdx.x == 0) tw = __builtin_amdgcn_s_memtime(); }
+  __device__ void wait_end(unsigned long long& acc) {
+    if (threadIdx.x == 0) acc += __builtin_amdgcn_s_memtime() - tw;
+  }
   __device__ AttnTrace() : t0(__builtin_amdgcn_s_memtime()), r0(__builtin_amdgcn_s_memrealtime()) {}
   __device__ ~AttnTrace() {
     const unsigned idx = blockIdx.y * gridDim.x + blockIdx.x;
@@ -286,8 +291,9 @@ struct AttnTrace {
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
     unsigned long long* p = g_attn_trace + 8 * (size_t)idx;
-    p[0] = r0; p[1] = r3; p[2] = t3 - t0; p[3] = (unsigned)blocks; p[4] = blockIdx.y; p[5] = blockIdx.x;
-    p[6] = ((unsigned long long)xcc << 32) | hw; p[7] = 1;
+    p[0] = r0; p[1] = r3; p[2] = t3 - t0; p[3] = (unsigned)blocks;
+    p[4] = ((unsigned long long)blockIdx.y << 32) | blockIdx.x; p[5] = (wv << 32) | (wk & 0xFFFFFFFFull);
+    p[6] = ((unsigned long long)xcc << 32) | hw; p[7] = ((ta ? ta - t0 : 0) << 32) | (t1 ? t1 - t0 : 0);
   }
 };
 #endif
@@ -320,6 +326,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   const int h = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
   const int b = tile.seq, len = vlen[b], base = soff[b];
+#ifdef LAYA_TILE_TRACE
+  asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(len), "s"(base) : "memory");
+  if (threadIdx.x == 0) at.ta = __builtin_amdgcn_s_memtime();
+#endif
 
   // this lane's query (32 per wave)
   const int r = wave * 32 + l32;
@@ -337,35 +347,45 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     hi_k = min(len, pmax + window_half + 1);
   }
 
-  // keys visible to this lane's query: [jlo, jhi)
-  const int jlo = (window_half > 0 && !gq) ? max(0, p - window_half) : 0;
-  const int jhi = (window_half > 0 && !gq) ? min(len, p + window_half + 1) : len;
+  // keys visible to this lane's query: [jlo, jhi).  Both bounds grow with the query, so every
+  // query of the tile sees [jlo_all, jhi_all): its last query's lower bound, its first one's upper.
+  const bool win = window_half > 0 && !gq;
+  const int jlo = win ? max(0, p - window_half) : 0;
+  const int jhi = win ? min(len, p + window_half + 1) : len;
+  const int jlo_all = win ? max(0, tile.q0 + tile.nq - 1 - window_half) : 0;
+  const int jhi_all = win ? min(len, tile.q0 + window_half + 1) : len;
 
-  // Q fragments (B operand): query row, d = 16 s + 8 hi .. + 7
-  const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(Q + (size_t)(base + p) * ldqk + h * HD);
+  // Q fragments (B operand): query row, d = 16 s + 8 hi .. + 7.  Loaded by inline assembly, so
+  // that the compiler's wait analysis does not count them: the wait before the key loop below
+  // (which is also what defines qf for the compiler) lets the first V^T block stay in flight.
+  const char* qa = reinterpret_cast<const char*>(Q + (size_t)(base + p) * ldqk + h * HD) + 16 * hi;
   u32x4_t qf[4];
-#pragma unroll
-  for (int s = 0; s < 4; s++) qf[s] = qrow[2 * s + hi];
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qf[0]) : "v"(qa) : "memory");
+  asm volatile("global_load_dwordx4 %0, %1, off offset:32" : "=v"(qf[1]) : "v"(qa) : "memory");
+  asm volatile("global_load_dwordx4 %0, %1, off offset:64" : "=v"(qf[2]) : "v"(qa) : "memory");
+  asm volatile("global_load_dwordx4 %0, %1, off offset:96" : "=v"(qf[3]) : "v"(qa) : "memory");
 
-  // DMA plan: instruction j (0..J-1 per wave) fills rows 8 (J wave + j) .. + 7 of the K block and
-  // of the V^T block; lane -> row + lane / 8, position lane % 8 (global chunk position ^ swizzle)
+  // DMA plan: instruction j (0..J-1 per wave) fills the 8 rows 8 g .. + 7 of the K block and of
+  // the V^T block, g = (wave & 1) + 2 (j + J (wave >> 1)); lane -> row 8 g + lane / 8, position
+  // lane % 8 (global chunk position ^ swizzle).  A wave's groups g all have the parity of its
+  // wave, so its lanes' swizzle is the same in all of them and instruction j's offset is the
+  // first one's plus 16 j rows: one offset register per operand.
   const u32x4_t rK = attn_rsrc(K, (uint32_t)((size_t)kv_rows * ldqk * 2));
   const u32x4_t rV = attn_rsrc(Vt, (uint32_t)((size_t)vt_rows * ldv * 2));
-  uint32_t kvo[J], vvo[J];
-#pragma unroll
-  for (int j = 0; j < J; j++) {
-    const int row = 8 * (J * wave + j) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
-    kvo[j] = ((uint32_t)(base + row) * (uint32_t)ldqk + (uint32_t)(h * HD)) * 2u + (uint32_t)c * 16u;
-    vvo[j] = ((uint32_t)(h * HD + row) * (uint32_t)ldv + (uint32_t)base) * 2u + (uint32_t)c * 16u;
-  }
-  const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)J * 1024u;
+  const int g0 = (wave & 1) + 2 * J * (wave >> 1);
+  const int row0 = 8 * g0 + (lane >> 3), c0 = (lane & 7) ^ ((row0 >> 1) & 7);
+  const uint32_t kvo = ((uint32_t)(base + row0) * (uint32_t)ldqk + (uint32_t)(h * HD)) * 2u + (uint32_t)c0 * 16u;
+  const uint32_t vvo = ((uint32_t)(h * HD + row0) * (uint32_t)ldv + (uint32_t)base) * 2u + (uint32_t)c0 * 16u;
+  const uint32_t wsl = (uint32_t)__builtin_amdgcn_readfirstlane(g0) * 1024u;
   auto fetch_k = [&](int k0, u32x4_t* ks) {
 #pragma unroll
-    for (int j = 0; j < J; j++) attn_dma16(rK, lds_addr_a(ks) + wsl + j * 1024, kvo[j] + (uint32_t)k0 * (uint32_t)ldqk * 2u);
+    for (int j = 0; j < J; j++)
+      attn_dma16(rK, lds_addr_a(ks) + wsl + j * 2048, kvo + (uint32_t)(k0 + 16 * j) * (uint32_t)ldqk * 2u);
   };
   auto fetch_v = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < J; j++) attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 1024, vvo[j] + (uint32_t)k0 * 2u);
+    for (int j = 0; j < J; j++)
+      attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 2048, vvo + (uint32_t)(16 * j) * (uint32_t)ldv * 2u + (uint32_t)k0 * 2u);
   };
 
   f32x16_t o[2], lsum;
@@ -375,24 +395,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     o[1][e] = 0.f;
     lsum[e] = 0.f;
   }
-  // running max of the raw scores (scale > 0 keeps the order); probabilities are
+  // m_run: a trailing running max of the raw scores (scale > 0 keeps the order); probabilities are
   // exp2(s * c - m * c) with c = scale * log2(e), one FMA per score.  The running sum of the
   // probabilities is an MFMA of an all-ones A operand with P^T (the MFMA pipe has room, the VALU
   // has none): every element of lsum holds the sum over the keys so far of this lane's query, summed
   // over exactly the bf16 values that the PV product uses.
   float m_run = -INFINITY;
+  constexpr float kLazyLog2 = 8.f;
   const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
   const float c2 = scale * 1.44269504088896340736f;
 
   fetch_k(lo, Ks0);
   fetch_v(lo);
-  // The Q fragments must be in registers before the key loop, and the compiler must know it.  Left
-  // to itself it sinks their loads to the loop entry, and its wait analysis then counts them as
-  // outstanding in every iteration: vmcnt(3..0) before the Q K^T MFMAs, which in later iterations
-  // wait for the next block's K fetch issued just before them.  Using the registers here makes it
-  // wait for the loads once, before the loop.
-  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Q and the first K block have landed (this wave's part); the first V^T block (the last J loads)
+  // may still be in flight: the first block waits for it before its PV step, so it lands while
+  // that block's scores and softmax run.  Loads complete in issue order.  The wait redefines qf,
+  // so no use of the Q registers can move above it.
+  if constexpr (J == 4)
+    asm volatile("s_waitcnt vmcnt(4)" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]) : : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(2)" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]) : : "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
@@ -403,11 +425,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   // operand of that step is one 16-byte chunk of each d row.
   const int krow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
   const int ksw = (krow >> 1) & 7;                         // swizzle of K rows 32 n + krow
-  // One 64-key block: S^T = K Q^T, online softmax (MASKED: with the per-query key range), O^T +=
-  // V^T P^T.  The masked and unmasked blocks are separate copies of the whole block, so that the
-  // scores go from the MFMA to the softmax in the registers the MFMA wrote them to.
-  auto block = [&](auto masked, int k0, bool more, const u32x4_t* ks) {
-    constexpr bool MASKED = decltype(masked)::value;
+  // One 64-key block: S^T = K Q^T, online softmax with the per-query key range, O^T += V^T P^T.
+  // MASK says which bounds of the range may cut into the block: 0 none, 2 the upper only, 3 both.
+  // The upper bound alone costs a compare and a select per score; both bounds, a subtract more.
+  // Each MASK is a separate copy of the whole block, so that the scores go from the MFMA to the
+  // softmax in the registers the MFMA wrote them to.
+  auto block = [&](auto mask, int k0, bool first, bool more, const u32x4_t* ks) {
+    constexpr int MASK = decltype(mask)::value;
+    // this lane's visible keys relative to key k0 + 8 hi, the first of its score elements
+    const int A = jlo - k0 - 8 * hi, B = jhi - k0 - 8 * hi;
     f32x16_t st[2];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
@@ -425,35 +451,53 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        if constexpr (MASKED) {
-          // visible keys of this lane's query: [jlo, jhi)
-          const int j = k0 + 32 * kb + 16 * (e >> 3) + 8 * hi + (e & 7);
-          st[kb][e] = (unsigned)(j - jlo) < (unsigned)(jhi - jlo) ? st[kb][e] : -INFINITY;
+        if constexpr (MASK != 0) {
+          // element e holds key k0 + 8 hi + c
+          const int c = 32 * kb + 16 * (e >> 3) + (e & 7);
+          bool vis;
+          if constexpr (MASK == 3) vis = (unsigned)(c - A) < (unsigned)(B - A);
+          else vis = c < B;
+          st[kb][e] = vis ? st[kb][e] : -INFINITY;
         }
         mx = fmaxf(mx, st[kb][e]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    // with no visible key yet (m_new = -inf) every exp2 below is exp2(-inf) = 0
-    const float mc = m_new == -INFINITY ? 0.f : m_new * c2;
+    {
+      // lanes l and l ^ 32 hold one query's scores: v_permlane32_swap gives every lane the value
+      // of lane l % 32 and of lane 32 + l % 32 (a VALU exchange; a shuffle would go through LDS)
+      const auto hl = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(hl[0]), __uint_as_float(hl[1]));
+    }
+    // m_run, the exponent's reference, trails the running max: it moves (to every lane's max, with
+    // the running output and sum rescaled) only when some valid query's max exceeds it by more
+    // than 2^kLazyLog2 in probability, so probabilities stay at most 2^kLazyLog2 and most blocks
+    // skip the 48 multiplies of the rescale.  The first block has nothing to rescale.  Lanes past
+    // the tile's last query stand in for its first query and do not vote, so the points where a
+    // wave moves m_run depend on its own queries only, whatever the tile size; the stand-ins track
+    // their own max (their output is dropped).
+    if (first) {
+      m_run = mx;
+    } else if (__any(qvalid && (mx - m_run) * c2 > kLazyLog2)) {
+      // (m_run = -inf with a visible key: +inf > kLazyLog2; with none: NaN, no vote)
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, m_new == -INFINITY ? 0.f : -m_new * c2));
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; db++) o[db] *= alpha;
+      m_run = m_new;
+    }
+    if (!qvalid) m_run = fmaxf(m_run, mx);
+    // with no visible key yet (m_run = -inf) every exp2 below is exp2(-inf) = 0
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) st[kb][e] = __builtin_amdgcn_exp2f(fmaf(st[kb][e], c2, -mc));
-    // the running output and sum are rescaled only when some valid query's max moved (alpha == 1
-    // otherwise, up to the rounding of m * c).  Lanes past the tile's last query stand in for its
-    // first query and do not vote, so the rescale points of a wave depend on its own queries only,
-    // whatever the tile size.
-    if (__any(qvalid && m_new != m_run)) {
-      const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, -mc));
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < 2; db++) o[db] *= alpha;
-    }
-    m_run = m_new;
 
     // this block's V^T (fetched after the previous PV step, before the K fetch) has landed in
     // every wave's part
+#ifdef LAYA_TILE_TRACE
+    at.wait_begin();
+#endif
     if (more) {
       if constexpr (J == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
@@ -462,6 +506,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+#ifdef LAYA_TILE_TRACE
+    at.wait_end(at.wv);
+#endif
 
     // ---- O^T += V^T P^T: four 16-key steps; step kk covers keys 16 kk + 8 hi + (0..7) in lane l ----
 #pragma unroll
@@ -483,19 +530,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 
   // One pass of the loop below: the block at k0 (K in buffer `it` % 2), then the fetches of the
   // next one.  Each call site of `block` holds its own copy of the whole block (no score register
-  // is shared between the masked and the unmasked copy).
+  // is shared between copies).
   int it = 0, k0 = lo;
-  auto step = [&](auto masked) {
+#ifdef LAYA_TILE_TRACE
+  if (threadIdx.x == 0) at.t1 = __builtin_amdgcn_s_memtime();
+#endif
+  auto step = [&](auto mask) {
     const bool odd = it & 1;
     const u32x4_t* ks = odd ? Ks1 : Ks0;
     const bool more = k0 + 64 < hi_k;
     // the other K buffer was last read by the previous block's scores, before its final barrier
     if (more) fetch_k(k0 + 64, odd ? Ks0 : Ks1);
-    block(masked, k0, more, ks);
+    block(mask, k0, it == 0, more, ks);
     // the next block's K has landed (this wave's part) and no wave still reads V^T or this K
+#ifdef LAYA_TILE_TRACE
+    at.wait_begin();
+#endif
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+#ifdef LAYA_TILE_TRACE
+    at.wait_end(at.wk);
+#endif
     if (more) fetch_v(k0 + 64);
     k0 += 64;
     ++it;
@@ -503,14 +559,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     at.blocks = it;
 #endif
   };
-  if (window_half > 0 && !gq) {
-    // sliding window: a tile's few blocks are mostly partly visible; all take the mask
-    while (k0 < hi_k) step(std::true_type{});
-  } else {
-    // global: every block but the last partial one is visible to every query
-    while (k0 + 64 <= hi_k) step(std::false_type{});
-    if (k0 < hi_k) step(std::true_type{});
-  }
+  // Three runs of blocks: those cut by the lower bound of some query's range (a sliding tile's
+  // first; they may be cut by the upper bound too, in a short question), those visible to every
+  // query (all of a global tile's but a last partial one; a sliding tile's middle one) and those
+  // cut only by the upper bound (a sliding tile's last, a global tile's partial last).  Three
+  // loops, not one loop choosing among the copies: with both copies in one loop body the
+  // registers no longer fit three waves per SIMD.
+  while (k0 < hi_k && k0 < jlo_all) step(std::integral_constant<int, 3>{});
+  while (k0 + 64 <= jhi_all) step(std::integral_constant<int, 0>{});
+  while (k0 < hi_k) step(std::integral_constant<int, 2>{});
 
   if (!qvalid) return;
   // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4

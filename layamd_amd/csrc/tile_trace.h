@@ -26,7 +26,12 @@ int laya_tile_trace_clear(void);
 /* The bf16 attention kernel (k_attention_bf16) keeps its own records, one per workgroup at index
  * blockIdx.y * gridDim.x + blockIdx.x (tile-major, heads fastest), 8 uint64 each:
  *   [0] start, [1] end (100 MHz real-time clock), [2] shader cycles entry to exit,
- *   [3] 64-key blocks processed, [4] tile index, [5] head, [6] XCC id << 32 | HW_ID, [7] 1. */
+ *   [3] 64-key blocks processed, [4] tile index << 32 | head,
+ *   [5] shader cycles wave 0 spent in the V^T wait + barrier before each PV step (summed) << 32 |
+ *       those in the wait + barrier at the end of each block (next K landed, buffers free),
+ *   [6] XCC id << 32 | HW_ID,
+ *   [7] shader cycles from entry to the tile's question offset and length loaded << 32 |
+ *       those from entry to the first key block (Q and the first K, V^T block loaded). */
 int laya_attn_trace_read(void* host, size_t records);
 int laya_attn_trace_clear(void);
 #ifdef __cplusplus
