@@ -82,7 +82,7 @@ def build_trace(jobs: int = 8, verbose: bool = True) -> str:
     return TRACE_LIB
 
 
-PROBES = {"gemm-wave-probe": "gemm_wave_probe.hip"}
+PROBES = {"gemm-wave-probe": "gemm_wave_probe.hip", "mfma-valu-probe": "mfma_valu_probe.hip"}
 
 
 def build_probes(verbose: bool = True) -> None:
