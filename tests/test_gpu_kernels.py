@@ -127,7 +127,7 @@ class Packed:
     """Questions packed as the engine packs them: question b owns rows soff[b] .. soff[b] + len - 1,
     soff a multiple of 8; V^T [H*64][ldv] with column = row and 64 columns of slack."""
 
-    def __init__(self, lens, H, dtype, seed, qzero=False):
+    def __init__(self, lens, H, dtype, seed, qzero=False, qscale=1.0, kramp=0.0):
         import torch
         self.lens = [int(x) for x in lens]
         self.H, self.D = H, 64 * H
@@ -136,8 +136,14 @@ class Packed:
         ldv = _up(self.rows + 64, 64)
         g = torch.Generator(device="cpu").manual_seed(seed)
         tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
-        q = torch.zeros(self.rows, self.D) if qzero else torch.randn(self.rows, self.D, generator=g)
+        q = torch.zeros(self.rows, self.D) if qzero else torch.randn(self.rows, self.D, generator=g) * qscale
         k = torch.randn(self.rows, self.D, generator=g)
+        if kramp:
+            # key j of a question scaled by 1 + kramp j / len: later keys score ever higher
+            ramp = torch.ones(self.rows)
+            for b, L in enumerate(self.lens):
+                ramp[self.soff[b]:self.soff[b] + L] = 1.0 + kramp * torch.arange(L) / L
+            k = k * ramp[:, None]
         v = torch.randn(self.rows, self.D, generator=g)
         self.q, self.k, self.v = (t.to(tdt) for t in (q, k, v))
         vt = torch.zeros(self.D, ldv, dtype=tdt)
@@ -211,6 +217,21 @@ def test_attention_edges(dtype, qtile, window_half, uniform):
     for b, L in enumerate(pk.lens):
         worst = max(worst, _check(pk, got[pk.soff[b]:pk.soff[b] + L], b, np.arange(L), window_half, uniform))
     print("attention edges %s q%d w%d uniform=%s: worst err/bound %.3f" % (dtype, qtile, window_half, uniform, worst))
+
+
+@pytest.mark.parametrize("dtype,qtile", [("bf16", 64), ("bf16", 128), ("fp32", 64)])
+@pytest.mark.parametrize("window_half", [64, 0])
+def test_attention_wide_score_range(dtype, qtile, window_half):
+    """Scores spread far wider than the random inputs' (Q x 4, keys growing in scale along each
+    question), so that a query's running maximum jumps by many times the bf16 kernel's trailing
+    threshold (2^8 in probability) from block to block and its output and sum are rescaled often,
+    with probabilities of earlier blocks underflowing; every query of every question."""
+    pk = Packed(EDGE_LENS + [511, 700], 2, dtype, seed=14, qscale=4.0, kramp=2.0)
+    got = pk.run(pk.encoder_tiles(qtile), window_half, qtile)
+    worst = 0.0
+    for b, L in enumerate(pk.lens):
+        worst = max(worst, _check(pk, got[pk.soff[b]:pk.soff[b] + L], b, np.arange(L), window_half, False))
+    print("attention wide scores %s q%d w%d: worst err/bound %.3f" % (dtype, qtile, window_half, worst))
 
 
 @pytest.mark.parametrize("workload,dtype,qtile", [("c3", "bf16", 64), ("c3", "bf16", 128), ("c4", "bf16", 64),
