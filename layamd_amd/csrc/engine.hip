@@ -165,7 +165,7 @@ struct Engine : EngineIface {
   // (so a captured graph's addresses hold for every replay of that shape) and uploaded by one copy
   int *d_ids, *d_pos, *d_seq, *d_soff, *d_vlen, *d_qt, *d_nm, *d_moff, *d_gq, *d_grow;
   int *h_ids, *h_pos, *h_seq, *h_soff, *h_vlen, *h_qt, *h_nm, *h_moff, *h_gq, *h_grow;
-  AttnTile *d_tiles, *d_gtiles, *h_tiles, *h_gtiles;
+  AttnTile *d_tiles, *d_gltiles, *d_gtiles, *h_tiles, *h_gltiles, *h_gtiles;
   char *d_blob = nullptr, *h_blob = nullptr;
   size_t blob_cap = 0;
   float *h_logits, *h_act;
@@ -456,9 +456,14 @@ struct Engine : EngineIface {
         lim.max_grows = (int)cap;
       }
     }
-    // attention query tiles: 64 queries (two waves in bf16); LAYA_ATTN_QTILE=128 gives bf16 128-query
-    // tiles of four waves, same bits, measured slower on sliding-window layers
-    lim.q_tile = sizeof(T) == 2 && env_int("LAYA_ATTN_QTILE", 64) == 128 ? 128 : 64;
+    // attention query tiles.  bf16: 64 queries (two waves) in the sliding-window layers and 128
+    // (four waves, four per SIMD) in the global ones, the faster tiling of each (same bits either
+    // way); LAYA_ATTN_QTILE=64 or 128 puts every layer on one of them.  fp32: 64.
+    {
+      const int qt = sizeof(T) == 2 ? env_int("LAYA_ATTN_QTILE", 0) : 64;
+      lim.q_tile = qt == 128 ? 128 : 64;
+      lim.q_tile_global = sizeof(T) == 2 && qt != 64 ? 128 : 64;
+    }
     if (lim.q_tile == 128 && (cfg.local_attention / 2) % 64 != 0) {
       // 128-query tiles visit the same key blocks as 64-query tiles only when the sliding window's
       // half width is a multiple of 64 (both tilings then start every query's keys on the same
@@ -527,7 +532,7 @@ struct Engine : EngineIface {
 
   // ------------------------------------------------------------ one pass
   // byte offsets of the index arrays of a pass bucket in the blocks (256-byte aligned)
-  struct BlobLayout { size_t ids, pos, seq, soff, vlen, qt, nm, moff, gq, grow, tiles, gtiles, total; };
+  struct BlobLayout { size_t ids, pos, seq, soff, vlen, qt, nm, moff, gq, grow, tiles, gltiles, gtiles, total; };
   static BlobLayout blob_layout(int rows, int B, int R, int nt, int ngt) {
     BlobLayout L;
     size_t o = 0;
@@ -536,7 +541,8 @@ struct Engine : EngineIface {
     L.soff = take((size_t)(B + 1) * 4); L.vlen = take((size_t)B * 4); L.qt = take((size_t)B * 4);
     L.nm = take((size_t)B * 4); L.moff = take((size_t)B * 4);
     L.gq = take((size_t)R * 4); L.grow = take((size_t)R * 4);
-    L.tiles = take((size_t)nt * sizeof(AttnTile)); L.gtiles = take((size_t)ngt * sizeof(AttnTile));
+    L.tiles = take((size_t)nt * sizeof(AttnTile)); L.gltiles = take((size_t)nt * sizeof(AttnTile));
+    L.gtiles = take((size_t)ngt * sizeof(AttnTile));
     L.total = o;
     return L;
   }
@@ -548,12 +554,14 @@ struct Engine : EngineIface {
     at(L.soff, &d_soff, &h_soff); at(L.vlen, &d_vlen, &h_vlen); at(L.qt, &d_qt, &h_qt);
     at(L.nm, &d_nm, &h_nm); at(L.moff, &d_moff, &h_moff); at(L.gq, &d_gq, &h_gq); at(L.grow, &d_grow, &h_grow);
     d_tiles = (AttnTile*)(d_blob + L.tiles); h_tiles = (AttnTile*)(h_blob + L.tiles);
+    d_gltiles = (AttnTile*)(d_blob + L.gltiles); h_gltiles = (AttnTile*)(h_blob + L.gltiles);
     d_gtiles = (AttnTile*)(d_blob + L.gtiles); h_gtiles = (AttnTile*)(h_blob + L.gtiles);
   }
 
   void stage_inputs(const PassPlan& p) {
     const Shape s{p.T, p.B, p.KT};
-    if ((int)p.tiles.size() != s.nt() || (int)p.gtiles.size() != s.ngt() || p.R != s.R() || (int)p.gq.size() > p.R) {
+    if ((int)p.tiles.size() != s.nt() || (int)p.gltiles.size() != s.nt() || (int)p.gtiles.size() != s.ngt() ||
+        p.R != s.R() || (int)p.gq.size() > p.R) {
       fprintf(stderr, "[laya] internal error: pass arrays do not match their bucket\n");
       exit(1);
     }
@@ -564,6 +572,7 @@ struct Engine : EngineIface {
     memcpy(h_nm, p.nm.data(), p.B * 4); memcpy(h_moff, p.moff.data(), p.B * 4);
     memcpy(h_gq, p.gq.data(), p.gq.size() * 4); memcpy(h_grow, p.grow.data(), p.R * 4);
     memcpy(h_tiles, p.tiles.data(), p.tiles.size() * sizeof(AttnTile));
+    memcpy(h_gltiles, p.gltiles.data(), p.gltiles.size() * sizeof(AttnTile));
     memcpy(h_gtiles, p.gtiles.data(), p.gtiles.size() * sizeof(AttnTile));
   }
 
@@ -799,8 +808,9 @@ struct Engine : EngineIface {
         GSTAGE("enc:gemm_qkv_rope", gemm(EPI_QKV, g, st));
       }
       STAGE(glob ? "enc:attn_global" : "enc:attn_sliding",
-            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt(), lim.q_tile, H, d_soff, d_vlen,
-                                nullptr, nullptr, glob ? 0 : cfg.local_attention / 2, scale, st));
+            launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, glob ? d_gltiles : d_tiles, s.nt(),
+                                glob ? lim.q_tile_global : lim.q_tile, H, d_soff, d_vlen, nullptr, nullptr,
+                                glob ? 0 : cfg.local_attention / 2, scale, st));
       {
         GemmArgs g = gemm_args(ao, D, e.Wo, T_, D, D, nullptr);
         g.X = x; g.ldx = D;
@@ -857,7 +867,7 @@ struct Engine : EngineIface {
         GSTAGE("head:gemm_qkv", gemm(EPI_QKV, g, st));
       }
       if (!last) {
-        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_tiles, s.nt(), lim.q_tile, H, d_soff,
+        STAGE("head:attn", launch_attention<T>(q, k, D, (int)MT, vt, (int)VTC, ao, D, d_gltiles, s.nt(), lim.q_tile_global, H, d_soff,
                                                d_vlen, nullptr, nullptr, 0, scale, st));
         { GemmArgs g = gemm_args(ao, D, hl.outW, T_, D, D, hl.outB); g.X = x; g.ldx = D;
           if (fold_ln) fold_out(g);

@@ -13,24 +13,27 @@ extern "C" {
 
 // Plans a laya_forward_batch call.  Returns -1 on invalid input, else the number of passes.
 // For pass `which` it fills (when the pointers are non-null and large enough):
-//   dims[10] = first, B, T, valid, KT, R, ntiles, ngtiles, len(gq), 0
+//   dims[10] = first, B, T, valid, KT, R, ntiles, ngtiles, len(gq), ngltiles
 //   rows[3*T] = ids | pos | seq; seqs[5*B+1] = soff(B+1) | vlen | qt | nm | moff
-//   tiles[4*ntiles], gtiles[4*ngtiles], gq[len], grow[R]
+//   tiles[4*ntiles] (sliding-window query tiles of <= q_tile), gltiles[4*ngltiles] (global query
+//   tiles of <= q_tile_global), gtiles[4*ngtiles], gq[len], grow[R]
 int laya_host_plan(int B, const int* lens, const int* ids, const int* nmark, const int* markers, const int* qtypes,
                    int max_len, int pass_tokens, int max_seqs, int max_grows, int vocab, int pad_id, int q_tile,
-                   int which, int* dims,
-                   int* rows, int* seqs, int* tiles, int* gtiles, int* gq, int* grow) {
+                   int q_tile_global, int which, int* dims,
+                   int* rows, int* seqs, int* tiles, int* gltiles, int* gtiles, int* gq, int* grow) {
   PackLimits lim;
   lim.max_len = max_len; lim.pass_tokens = pass_tokens; lim.max_seqs = max_seqs; lim.max_grows = max_grows;
   lim.vocab = vocab;
   lim.pad_id = pad_id;
   lim.q_tile = q_tile;
+  lim.q_tile_global = q_tile_global;
   std::vector<PassPlan> ps;
   if (plan_passes(B, lens, ids, nmark, markers, qtypes, lim, &ps) != 0) return -1;
   if (which >= 0 && which < (int)ps.size()) {
     const PassPlan& p = ps[which];
     if (dims) {
-      int d[10] = {p.first, p.B, p.T, p.valid, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size(), (int)p.gq.size(), 0};
+      int d[10] = {p.first, p.B, p.T, p.valid, p.KT, p.R, (int)p.tiles.size(), (int)p.gtiles.size(), (int)p.gq.size(),
+                   (int)p.gltiles.size()};
       memcpy(dims, d, sizeof d);
     }
     if (rows) {
@@ -46,6 +49,7 @@ int laya_host_plan(int B, const int* lens, const int* ids, const int* nmark, con
       memcpy(s, p.moff.data(), p.B * 4);
     }
     if (tiles) memcpy(tiles, p.tiles.data(), p.tiles.size() * sizeof(AttnTile));
+    if (gltiles) memcpy(gltiles, p.gltiles.data(), p.gltiles.size() * sizeof(AttnTile));
     if (gtiles) memcpy(gtiles, p.gtiles.data(), p.gtiles.size() * sizeof(AttnTile));
     if (gq) memcpy(gq, p.gq.data(), p.gq.size() * 4);
     if (grow) memcpy(grow, p.grow.data(), p.R * 4);

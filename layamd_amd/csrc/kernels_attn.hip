@@ -225,11 +225,11 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 // ======================================================================================
 // bf16 attention (v_mfma_f32_32x32x16_bf16).  One workgroup of NW waves owns one query tile (<= 32 NW
 // queries of one sequence) of one head; each wave owns 32 queries, so every K and V^T fragment read
-// from LDS feeds a 32-query MFMA.  NW = 2 (64-query tiles) is the engine's choice.  NW = 4 (128-query
-// tiles, encoder only) walks 256 keys for 128 queries in a sliding-window layer instead of 192 for 64
-// and fetches each key block once per 128 queries in a global one; it measured 3% faster on global
-// layers and 8% slower on sliding ones (a tile's blocks run one after another, and half as many
-// workgroups hide less of each block's fetch latency).  A query's blocks are the same in both
+// from LDS feeds a 32-query MFMA.  The engine runs NW = 2 (64-query tiles) in sliding-window layers
+// and NW = 4 (128-query tiles, four waves per SIMD) in global ones: a 128-query tile fetches each
+// key block once per 128 queries (global layers 5% faster), but walks 256 keys for 128 queries in a
+// sliding-window layer instead of 192 for 64 (3% slower there: a tile's blocks run one after
+// another, and half as many workgroups hide less of each block's fetch latency).  A query's blocks are the same in both
 // tilings but for blocks masked for every query of its wave, which add exact zeros and move no
 // maximum, so both give the same bits.  Keys advance in blocks of 64, fetched by LDS DMA
 // (inline assembly, as in the GEMM): the next block's K while the current block is scored, the next
@@ -241,13 +241,14 @@ __device__ __forceinline__ uint32_t lds_addr_a(const void* p) {
 // The 32x32 accumulator gives lane l query l % 32 and rows 8 (e / 4) + 4 (l / 32) + e % 4 of a
 // 32-key sub-block; the K operand's rows are permuted so that these rows are keys
 // 16 (e / 8) + 8 (l / 32) + e % 8.  Lanes l and l ^ 32 together hold a query's 64 scores: the row
-// max takes one cross-lane step, and the row sum is one more MFMA per PV step (an all-ones A operand
-// times P^T).  Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand of one 16-key PV
+// max takes one cross-lane step, and each lane sums its half of the probabilities, added to the
+// other half's at the end.  Eight accumulator elements (e = 8 h' .. 8 h' + 7) are the B operand of one 16-key PV
 // step with k-index i <-> key 16 h' + i, so the V^T operand of that step is one 16-byte LDS read per
 // lane.  Scores are scaled into the log2 domain once (exp2).  Global layers' blocks but the last
 // partial one skip the mask; sliding-window blocks all take it.
 // ======================================================================================
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // LDS DMA of one 16-byte chunk per lane (see the GEMM's dma16: the LDS base is an operand bound
 // to M0, the whole offset is range-checked, the memory clobber orders it against LDS reads)
@@ -299,7 +300,7 @@ struct AttnTrace {
 #endif
 
 template <int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 4 : 3, 8))) void k_attention_bf16(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K,
                                                         int ldqk, int kv_rows, const bf16_t* __restrict__ Vt, int ldv,
                                                         int vt_rows, bf16_t* __restrict__ O, int ldo,
                                                         const AttnTile* __restrict__ tiles, const int* __restrict__ soff,
@@ -313,8 +314,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   // distinct 16-byte bank positions
   // K is double-buffered (the next block's K is fetched while the current one is used); V^T has
   // one buffer, refilled right after the PV step and landing while the next block's scores and
-  // softmax run.  24 KB per workgroup: the VGPR limit (three waves per SIMD) fits six two-wave or
-  // three four-wave workgroups on a CU.
+  // softmax run.  24 KB per workgroup: six two-wave workgroups fit a CU (LDS, and three waves per
+  // SIMD within the 168-VGPR limit), four four-wave ones (four waves per SIMD in 128 VGPRs).
   __shared__ u32x4_t Ks0[64 * 8], Ks1[64 * 8], Vs[64 * 8];
 
 #ifdef LAYA_TILE_TRACE
@@ -388,21 +389,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
       attn_dma16(rV, lds_addr_a(Vs) + wsl + j * 2048, vvo + (uint32_t)(16 * j) * (uint32_t)ldv * 2u + (uint32_t)k0 * 2u);
   };
 
-  f32x16_t o[2], lsum;
+  f32x16_t o[2];
 #pragma unroll
   for (int e = 0; e < 16; e++) {
     o[0][e] = 0.f;
     o[1][e] = 0.f;
-    lsum[e] = 0.f;
   }
   // m_run: a trailing running max of the raw scores (scale > 0 keeps the order); probabilities are
   // exp2(s * c - m * c) with c = scale * log2(e), one FMA per score.  The running sum of the
-  // probabilities is an MFMA of an all-ones A operand with P^T (the MFMA pipe has room, the VALU
-  // has none): every element of lsum holds the sum over the keys so far of this lane's query, summed
-  // over exactly the bf16 values that the PV product uses.
+  // probabilities is summed over exactly the bf16 values that the PV product uses, two at a time
+  // (v_dot2c_f32_bf16 with (1, 1): a bf16 pair's sum added in fp32), into two partial sums per lane
+  // (even and odd pairs): lane l holds the keys 8 (l / 32) .. + 7 of each 16-key step, so a
+  // query's sum is lane l's plus lane l ^ 32's, taken once at the end.
+  float lsum[2] = {0.f, 0.f};
   float m_run = -INFINITY;
   constexpr float kLazyLog2 = 8.f;
-  const bf16x8_t ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+  const bf16x2_t one2 = {(__bf16)1.f, (__bf16)1.f};
   const float c2 = scale * 1.44269504088896340736f;
 
   fetch_k(lo, Ks0);
@@ -480,7 +482,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
       // (m_run = -inf with a visible key: +inf > kLazyLog2; with none: NaN, no vote)
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(fmaf(m_run, c2, m_new == -INFINITY ? 0.f : -m_new * c2));
-      lsum *= alpha;
+      lsum[0] *= alpha;
+      lsum[1] *= alpha;
 #pragma unroll
       for (int db = 0; db < 2; db++) o[db] *= alpha;
       m_run = m_new;
@@ -524,7 +527,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
         const u32x4_t va = Vs[d * 8 + ((2 * kk + hi) ^ ((d >> 1) & 7))];
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, va), pb, o[db], 0, 0, 0);
       }
-      lsum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, pb, lsum, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const bf16x2_t pr = {pb[2 * q], pb[2 * q + 1]};
+        lsum[q & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, lsum[q & 1], false);
+      }
     }
   };
 
@@ -571,7 +578,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 
   if (!qvalid) return;
   // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4
-  const float l_run = lsum[0];
+  // the query's sum: this lane's and lane l ^ 32's (v_permlane32_swap: the values of lanes l % 32
+  // and 32 + l % 32, added in that order in both lanes)
+  const float lh = lsum[0] + lsum[1];
+  const auto lp = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
+  const float l_run = __uint_as_float(lp[0]) + __uint_as_float(lp[1]);
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   bf16_t* orow_p = O + (size_t)orow * ldo + h * HD;
 #pragma unroll

@@ -55,6 +55,8 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
         p.ids[r + j] = j < len ? ids[ioff[b] + j] : pad_id; p.pos[r + j] = j; p.seq[r + j] = i;
       }
       for (int q0 = 0; q0 < len; q0 += lim.q_tile) p.tiles.push_back({i, q0, std::min(lim.q_tile, len - q0), 0});
+      for (int q0 = 0; q0 < len; q0 += lim.q_tile_global)
+        p.gltiles.push_back({i, q0, std::min(lim.q_tile_global, len - q0), 0});
       r += rows; mo += nmark[b]; p.valid += len;
     }
     p.soff[n] = r;
@@ -79,9 +81,11 @@ int plan_passes(int B, const int* lens, const int* ids, const int* nmark, const 
     // any result)
     auto by_len = [&](const AttnTile& x, const AttnTile& y) { return p.vlen[x.seq] > p.vlen[y.seq]; };
     std::stable_sort(p.tiles.begin(), p.tiles.end(), by_len);
+    std::stable_sort(p.gltiles.begin(), p.gltiles.end(), by_len);
     std::stable_sort(p.gtiles.begin(), p.gtiles.end(), by_len);
     // empty tiles up to the bucket's capacities (the launch grids)
     p.tiles.resize(tiles_cap(p.T, n), AttnTile{0, 0, 0, 0});
+    p.gltiles.resize(tiles_cap(p.T, n), AttnTile{0, 0, 0, 0});
     p.gtiles.resize(gtiles_cap(p.R, n), AttnTile{0, 0, 0, 0});
     passes->push_back(std::move(p));
     b0 += n;

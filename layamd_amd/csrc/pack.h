@@ -11,7 +11,9 @@
 //     and every aligned group of kRowAlign rows belongs to one question, so the GEMM epilogue can
 //     write V^T [H][head_dim][rows] (column = row) with 16-byte stores;
 //   * attention work is a list of query tiles (seq, first query, query count) of <= q_tile
-//     queries (64; 128 on request for the bf16 engine); gathered tiles hold <= 64 queries;
+//     queries for the sliding-window layers (64; 128 on request for the bf16 engine) and one of
+//     <= q_tile_global queries for the global layers (128 in the bf16 engine, 64 in fp32);
+//     gathered tiles hold <= 64 queries;
 //   * the last head layer works on R = KT + B gathered rows: the sum(nmark) marker rows in
 //     question order, padded with copies of row 0 to KT rows (a multiple of kMarkerBucket), then
 //     one CLS row per question; gathered query tiles index a list of gathered-row ids;
@@ -46,7 +48,8 @@ struct PackLimits {
   int max_grows = 32768;             // gathered rows (sum of nmark + 1) per pass
   int vocab = 0;                     // > 0: ids must lie in [0, vocab)
   int pad_id = 0;                    // token id of padding rows
-  int q_tile = kQTile;               // queries per encoder / head-0 attention tile (64 or 128)
+  int q_tile = kQTile;               // queries per sliding-window attention tile (64 or 128)
+  int q_tile_global = kQTile;        // queries per global attention tile (encoder, head 0; 64 or 128)
 };
 
 struct AttnTile { int32_t seq, q0, nq, pad; };
@@ -58,7 +61,8 @@ struct PassPlan {
   int markers = 0;                   // sum of nmark (KT before padding)
   std::vector<int32_t> ids, pos, seq;                       // [T]
   std::vector<int32_t> soff, vlen, qt, nm, moff;            // [B] (soff has B + 1)
-  std::vector<AttnTile> tiles;                              // encoder / head-0 query tiles (tiles_cap)
+  std::vector<AttnTile> tiles;                              // sliding-window query tiles (tiles_cap)
+  std::vector<AttnTile> gltiles;                            // global query tiles (tiles_cap)
   std::vector<AttnTile> gtiles;                             // gathered query tiles (gtiles_cap)
   std::vector<int32_t> gq;                                  // gathered ids referenced by gtiles
   std::vector<int32_t> grow;                                // [R] packed row of each gathered row

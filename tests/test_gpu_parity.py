@@ -567,19 +567,22 @@ def test_tile_configs_bit_identical():
 
 
 def test_attention_query_tiles_bit_identical():
-    """The bf16 encoder attention runs 64-query tiles of two waves; 128-query tiles of four waves
-    (LAYA_ATTN_QTILE=128) visit the same key blocks for every query but for blocks masked for all
-    queries of its wave, which add exact zeros.  Whole passes must agree bit for bit: the b32 x s512
-    batch on ModernBERT-large (sliding and global layers), four 1024-context questions of the base
-    shape, and tiny questions whose lengths sit on either side of the 64- and 128-query edges."""
+    """The bf16 engine runs 64-query tiles of two waves in its sliding-window layers and 128-query
+    tiles of four waves in its global ones (LAYA_ATTN_QTILE=64 or 128 puts every layer on one
+    tiling).  Both tilings visit the same key blocks for every query but for blocks masked for all
+    queries of its wave, which add exact zeros.  Whole passes must agree bit for bit in all three
+    settings: the b32 x s512 batch on ModernBERT-large (sliding and global layers), four
+    1024-context questions of the base shape, and tiny questions whose lengths sit on either side
+    of the 64- and 128-query edges."""
     cases = [("large", wl.c3(0)), ("base", wl.c4(0).subset([0, 1, 2, 3])),
              ("tiny", wl.make_batch(ck.PRESETS["tiny"], [1, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 320],
                                     [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12], seed=5))]
     for tag, b in cases:
-        lo64, ac64 = engine(tag, "bf16", LAYA_GRAPHS=0).forward_flat(*b.flat())
-        lo128, ac128 = engine(tag, "bf16", LAYA_GRAPHS=0, LAYA_ATTN_QTILE=128).forward_flat(*b.flat())
-        assert np.isfinite(lo128).all() and np.isfinite(ac128).all(), tag
-        assert np.array_equal(lo128, lo64) and np.array_equal(ac128, ac64), tag
+        lo64, ac64 = engine(tag, "bf16", LAYA_GRAPHS=0, LAYA_ATTN_QTILE=64).forward_flat(*b.flat())
+        assert np.isfinite(lo64).all() and np.isfinite(ac64).all(), tag
+        for qt in (None, 128):
+            lo, ac = engine(tag, "bf16", LAYA_GRAPHS=0, LAYA_ATTN_QTILE=qt).forward_flat(*b.flat())
+            assert np.array_equal(lo, lo64) and np.array_equal(ac, ac64), (tag, qt)
 
 
 def test_ln_fold_bits():

@@ -21,7 +21,7 @@ def host():
         build.build()
     L = ctypes.CDLL(le.HOST_LIB)
     IP = ctypes.POINTER(ctypes.c_int)
-    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 8 + [IP] * 7
+    L.laya_host_plan.argtypes = [ctypes.c_int, IP, IP, IP, IP, IP] + [ctypes.c_int] * 9 + [IP] * 8
     L.laya_host_plan.restype = ctypes.c_int
     L.laya_host_config.argtypes = [ctypes.c_char_p, IP, ctypes.POINTER(ctypes.c_float), ctypes.c_char_p, ctypes.c_int]
     L.laya_host_config.restype = ctypes.c_int
@@ -38,10 +38,11 @@ def P(a):
 
 
 def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=512, max_grows=32768, vocab=0,
-         pad_id=0, q_tile=64):
+         pad_id=0, q_tile=64, q_tile_global=None):
     keep = [P(x if len(x) else [0]) for x in (lens, ids, nm, mk, qt)]
-    args = (max_len, pass_tokens, max_seqs, max_grows, vocab, pad_id, q_tile)
-    n = host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, -1, *([None] * 7))
+    args = (max_len, pass_tokens, max_seqs, max_grows, vocab, pad_id, q_tile,
+            q_tile if q_tile_global is None else q_tile_global)
+    n = host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, -1, *([None] * 8))
     if n < 0:
         return None
     out = []
@@ -52,18 +53,20 @@ def plan(host, lens, ids, nm, mk, qt, max_len=512, pass_tokens=65536, max_seqs=5
         rows = np.zeros(3 * T, np.int32)
         seqs = np.zeros(5 * len(lens) + 1, np.int32)
         tiles = np.zeros(4 * (T // 64 + len(lens)), np.int32)
+        gltiles = np.zeros(4 * (T // 64 + len(lens)), np.int32)
         gtiles = np.zeros(4 * (R // 64 + len(lens)), np.int32)
         gq = np.zeros(R, np.int32)
         grow = np.zeros(R, np.int32)
-        bufs = [P(x)[1] for x in (dims, rows, seqs, tiles, gtiles, gq, grow)]
+        bufs = [P(x)[1] for x in (dims, rows, seqs, tiles, gltiles, gtiles, gq, grow)]
         host.laya_host_plan(len(lens), *[k[1] for k in keep], *args, w, *bufs)
-        first, B, Tn, valid, KT, Rn, nt, ngt, ngq, _ = dims
+        first, B, Tn, valid, KT, Rn, nt, ngt, ngq, nglt = dims
         s = seqs[:5 * B + 1]
         out.append(dict(first=first, B=B, T=Tn, valid=valid, KT=KT, R=Rn,
                         ids=rows[:Tn], pos=rows[Tn:2 * Tn], seq=rows[2 * Tn:3 * Tn],
                         soff=s[:B + 1], vlen=s[B + 1:2 * B + 1], qt=s[2 * B + 1:3 * B + 1],
                         nm=s[3 * B + 1:4 * B + 1], moff=s[4 * B + 1:5 * B + 1],
-                        tiles=tiles[:4 * nt].reshape(-1, 4), gtiles=gtiles[:4 * ngt].reshape(-1, 4),
+                        tiles=tiles[:4 * nt].reshape(-1, 4), gltiles=gltiles[:4 * nglt].reshape(-1, 4),
+                        gtiles=gtiles[:4 * ngt].reshape(-1, 4),
                         gq=gq[:ngq], grow=grow[:Rn]))
     return out
 
@@ -87,11 +90,11 @@ def up64(x):
     return (int(x) + 63) // 64 * 64
 
 
-@pytest.mark.parametrize("q_tile", [64, 128])
-def test_layout_of_a_pass(host, q_tile):
+@pytest.mark.parametrize("q_tile,q_tile_global", [(64, 64), (64, 128), (128, 128)])
+def test_layout_of_a_pass(host, q_tile, q_tile_global):
     cfg = ck.PRESETS["tiny"]
     b = wl.make_batch(cfg, [1, 64, 65, 200, 17, 128, 129, 256], [1, 3, 255, 12, 2, 1, 4, 2], seed=1)
-    (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, q_tile=q_tile)
+    (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, q_tile=q_tile, q_tile_global=q_tile_global)
     rows8 = (b.lens + 7) // 8 * 8                                          # questions start on 8-row groups
     # the pass's rows are padded to a multiple of 64 (its graph bucket)
     assert p["B"] == b.B and p["T"] == up64(rows8.sum()) and p["valid"] == int(b.lens.sum())
@@ -106,19 +109,22 @@ def test_layout_of_a_pass(host, q_tile):
         assert np.array_equal(p["pos"][r], np.arange(rows8[i]))
         assert np.all(p["seq"][r] == i)
         assert soff[i] % 8 == 0
-    # encoder tiles: every valid row of every question exactly once, <= q_tile queries, inside its
-    # question, a full tile unless it holds the question's last row; the list is padded with empty
-    # tiles to the bucket's capacity T / 64 + B
-    assert len(p["tiles"]) == p["T"] // 64 + b.B
-    real = p["tiles"][p["tiles"][:, 2] > 0]
-    assert np.all(p["tiles"][len(real):] == 0)
-    cover = np.zeros(p["T"], int)
-    for seq, q0, nq, _ in real:
-        assert 1 <= nq <= q_tile and q0 % q_tile == 0 and q0 + nq <= b.lens[seq]
-        assert nq == q_tile or q0 + nq == b.lens[seq]
-        cover[soff[seq] + q0: soff[seq] + q0 + nq] += 1
+    # encoder tiles (sliding-window layers: <= q_tile queries; global layers: <= q_tile_global):
+    # every valid row of every question exactly once, inside its question, a full tile unless it
+    # holds the question's last row, longest questions first; each list is padded with empty tiles
+    # to the bucket's capacity T / 64 + B
     valid_rows = np.concatenate([np.arange(soff[i], soff[i] + b.lens[i]) for i in range(b.B)])
-    assert np.all(cover[valid_rows] == 1) and cover.sum() == p["valid"]
+    for key, qtl in (("tiles", q_tile), ("gltiles", q_tile_global)):
+        assert len(p[key]) == p["T"] // 64 + b.B
+        real = p[key][p[key][:, 2] > 0]
+        assert np.all(p[key][len(real):] == 0)
+        assert np.all(np.diff(b.lens[real[:, 0]]) <= 0)
+        cover = np.zeros(p["T"], int)
+        for seq, q0, nq, _ in real:
+            assert 1 <= nq <= qtl and q0 % qtl == 0 and q0 + nq <= b.lens[seq]
+            assert nq == qtl or q0 + nq == b.lens[seq]
+            cover[soff[seq] + q0: soff[seq] + q0 + nq] += 1
+        assert np.all(cover[valid_rows] == 1) and cover.sum() == p["valid"]
     # gathered rows: markers in question order, padded with row 0 to a multiple of 64, then one CLS
     # row per question
     nmk = int(b.nmark.sum())
