@@ -576,13 +576,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4
   while (k0 + 64 <= jhi_all) step(std::integral_constant<int, 0>{});
   while (k0 < hi_k) step(std::integral_constant<int, 2>{});
 
-  if (!qvalid) return;
-  // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4
-  // the query's sum: this lane's and lane l ^ 32's (v_permlane32_swap: the values of lanes l % 32
-  // and 32 + l % 32, added in that order in both lanes)
+  // the query's sum: this lane's and lane l ^ 32's (v_permlane32_swap, with every lane still
+  // active: the values of lanes l % 32 and 32 + l % 32, added in that order in both lanes)
   const float lh = lsum[0] + lsum[1];
   const auto lp = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
   const float l_run = __uint_as_float(lp[0]) + __uint_as_float(lp[1]);
+  if (!qvalid) return;
+  // o[db][e] = O^T[d = 32 db + 8 (e / 4) + 4 hi + e % 4][query]: 4 consecutive d per e / 4
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   bf16_t* orow_p = O + (size_t)orow * ldo + h * HD;
 #pragma unroll
