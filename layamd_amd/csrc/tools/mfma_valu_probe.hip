@@ -46,7 +46,7 @@ __device__ __forceinline__ void fma_(float& x, float m, float c) {
 
 // MODE: 0 mfma, 1 valu, 2 inter, 3 phases
 template <int MODE, bool AGPR>
-__global__ __launch_bounds__(256) void k_probe(float* out, unsigned long long* cyc, int iters) {
+__global__ __launch_bounds__(256) void k_probe(float* out, int iters) {
   const int lane = threadIdx.x & 63;
   bf16x8_t a, b;
   for (int i = 0; i < 8; i++) {
@@ -87,22 +87,21 @@ __global__ __launch_bounds__(256) void k_probe(float* out, unsigned long long* c
     for (int e = 0; e < 16; e++) s += acc[k][e];
   for (int i = 0; i < 8; i++) s += x[i];
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
-  if (threadIdx.x == 0) cyc[blockIdx.x] = 0;
 }
 
 // nanoseconds per iteration: the launch's device time (one round of workgroups, all resident at
 // once) over the iterations, the median of 5 launches after a warm-up launch
 template <int MODE, bool AGPR>
-static double run(int per_cu, int cus, float* out, unsigned long long* cyc) {
+static double run(int per_cu, int cus, float* out) {
   const int grid = per_cu * cus;
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  hipLaunchKernelGGL((k_probe<MODE, AGPR>), dim3(grid), dim3(256), 0, 0, out, cyc, ITERS);  // warm-up
+  hipLaunchKernelGGL((k_probe<MODE, AGPR>), dim3(grid), dim3(256), 0, 0, out, ITERS);  // warm-up
   std::vector<double> t;
   for (int r = 0; r < 5; r++) {
     CHECK(hipEventRecord(e0, 0));
-    hipLaunchKernelGGL((k_probe<MODE, AGPR>), dim3(grid), dim3(256), 0, 0, out, cyc, ITERS);
+    hipLaunchKernelGGL((k_probe<MODE, AGPR>), dim3(grid), dim3(256), 0, 0, out, ITERS);
     CHECK(hipEventRecord(e1, 0));
     CHECK(hipEventSynchronize(e1));
     float ms = 0.f;
@@ -120,20 +119,18 @@ int main() {
   int cus = 0;
   CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
   float* out;
-  unsigned long long* cyc;
   CHECK(hipMalloc(&out, (size_t)3 * cus * 256 * sizeof(float)));
-  CHECK(hipMalloc(&cyc, (size_t)3 * cus * sizeof(unsigned long long)));
   printf("ns per iteration (each wave: %d MFMA 32x32x16 bf16, %d v_fma_f32 per iteration; the MFMAs of all\n"
          "the waves of a SIMD take %d matrix-core cycles per wave at 32 cycles each)\n", NM, NV, NM * 32);
   for (int agpr = 0; agpr < 2; agpr++) {
     for (int w = 1; w <= 3; w++) {
       double tm, tv, ti, tp;
       if (agpr) {
-        tm = run<0, true>(w, cus, out, cyc); tv = run<1, true>(w, cus, out, cyc);
-        ti = run<2, true>(w, cus, out, cyc); tp = run<3, true>(w, cus, out, cyc);
+        tm = run<0, true>(w, cus, out); tv = run<1, true>(w, cus, out);
+        ti = run<2, true>(w, cus, out); tp = run<3, true>(w, cus, out);
       } else {
-        tm = run<0, false>(w, cus, out, cyc); tv = run<1, false>(w, cus, out, cyc);
-        ti = run<2, false>(w, cus, out, cyc); tp = run<3, false>(w, cus, out, cyc);
+        tm = run<0, false>(w, cus, out); tv = run<1, false>(w, cus, out);
+        ti = run<2, false>(w, cus, out); tp = run<3, false>(w, cus, out);
       }
       printf("acc in %s, %d wave(s)/SIMD: mfma %7.1f  valu %7.1f  inter %7.1f  phases %7.1f | "
              "no overlap (mfma + valu) %7.1f, full overlap (max) %7.1f\n",
@@ -141,6 +138,5 @@ int main() {
     }
   }
   CHECK(hipFree(out));
-  CHECK(hipFree(cyc));
   return 0;
 }
