@@ -24,8 +24,9 @@ Output (data only; no reference code is copied):
       by the reference in fp32 and under bf16 autocast: fp32 and autocast logits and act logits,
       and per layer the reference's own bf16 drift over all valid rows, max |x_bf16 - x_fp32| /
       rms(x_fp32 row) (scalars only; the engine's fp32 side is the oracle on the GPU host).
-  tests/golden/<c3|c4>_full/drift.npz              the same record for every question of the
-      b32 x s512 and b16 x s1024 batches (32 and 16 questions; lengths up to 510 and 1020).
+  tests/golden/<c3|c4|c5>_full/drift.npz           the same record for every question of the
+      b32 x s512, b16 x s1024 and b64 varlen batches (32, 16 and 64 questions; lengths up to 510,
+      1020 and 1024).
 """
 import argparse
 import json
@@ -211,8 +212,9 @@ def batch_drift(out_root, work, preset, batch, tag):
 # questions of the bf16 benchmark batches whose reference bf16 drift is recorded
 DRIFT_SAMPLES = {"c3_sample": ("large", "c3", [0, 1, 2, 3]), "c4_sample": ("base", "c4", [11, 15]),
                  "c5_sample": ("large1024", "c5", [50, 17, 24]),
-                 # every question of the two fixed-length benchmark batches (b32 x s512, b16 x s1024)
-                 "c3_full": ("large", "c3", list(range(32))), "c4_full": ("base", "c4", list(range(16)))}
+                 # every question of the benchmark batches (b32 x s512, b16 x s1024, b64 varlen)
+                 "c3_full": ("large", "c3", list(range(32))), "c4_full": ("base", "c4", list(range(16))),
+                 "c5_full": ("large1024", "c5", list(range(64)))}
 
 
 def main():

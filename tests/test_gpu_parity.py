@@ -648,12 +648,13 @@ def test_gemm_tuning_keeps_outputs():
 
 # questions of the bf16 benchmark batches with the reference's bf16 drift recorded
 # (tests/golden/<tag>/drift.npz, written by make_golden.py): (checkpoint preset, batch, questions);
-# the *_full records hold every question of the b32 x s512 and b16 x s1024 batches
+# the *_full records hold every question of the b32 x s512, b16 x s1024 and b64 varlen batches
 SAMPLES = {"c3_sample": ("large", wl.c3, [0, 1, 2, 3]), "c4_sample": ("base", wl.c4, [11, 15]),
            "c5_sample": ("large1024", wl.c5, [50, 17, 24]),
-           "c3_full": ("large", wl.c3, list(range(32))), "c4_full": ("base", wl.c4, list(range(16)))}
+           "c3_full": ("large", wl.c3, list(range(32))), "c4_full": ("base", wl.c4, list(range(16))),
+           "c5_full": ("large1024", wl.c5, list(range(64)))}
 # for a whole-batch record, the sample whose questions must give the same bits inside the full pass
-SUBSET_OF_FULL = {"c3_full": "c3_sample", "c4_full": "c4_sample"}
+SUBSET_OF_FULL = {"c3_full": "c3_sample", "c4_full": "c4_sample", "c5_full": "c5_sample"}
 
 
 @pytest.mark.parametrize("tag", list(SAMPLES))
@@ -661,11 +662,11 @@ def test_bf16_sample_layer_drift(tag):
     """bf16 engine on questions of the b32 x s512 (ModernBERT-large), b16 x s1024 (mmBERT-base) and
     b64 varlen (ModernBERT-large-1024, 25-29 markers per sequence) batches: every valid row of every
     layer against the fp32 CPU oracle, within BF16_VS_UPSTREAM times the reference's own bf16 drift
-    on the same questions; logits and act logits likewise.  The c3_full and c4_full records cover
-    every question of the b32 x s512 and b16 x s1024 batches (C3's longest question has 510
-    tokens), run as the one pass bench.py times; the sampled questions must give the same bits
-    inside that pass as in their own.  For the varlen batch the whole 64-sequence pass (18k tokens)
-    must give the same bits for the sampled questions."""
+    on the same questions; logits and act logits likewise.  The *_full records cover every question
+    of the b32 x s512, b16 x s1024 and b64 varlen batches (C3's longest question has 510 tokens,
+    C5's 1024), each run as one pass as bench.py times it; the sampled questions must give the same
+    bits inside that pass as in their own.  For the varlen batch the whole 64-sequence pass (18k
+    tokens) must give the same bits for the sampled questions."""
     import torch
     from oracle import model as om
     torch.set_num_threads(min(16, os.cpu_count() or 1))
@@ -729,10 +730,11 @@ def test_bf16_sample_layer_drift(tag):
         assert np.array_equal(ac.reshape(full.B, -1)[sub], sac.reshape(len(sub), -1))
 
 
-@pytest.mark.parametrize("tag", ["c3_full", "c4_full"])
+@pytest.mark.parametrize("tag", ["c3_full", "c4_full", "c5_full"])
 def test_fp32_full_batch_vs_reference(tag):
-    """fp32 engine on every question of the b32 x s512 (ModernBERT-large) and b16 x s1024
-    (mmBERT-base) batches in one pass, against the logits and act logits the reference's own fp32
+    """fp32 engine on every question of the b32 x s512 (ModernBERT-large), b16 x s1024
+    (mmBERT-base) and b64 varlen (ModernBERT-large-1024) batches in one pass, against the logits
+    and act logits the reference's own fp32
     PyTorch model produced for the same inputs (tests/golden/<tag>/drift.npz): probabilities within
     1e-4 and act logits within 1e-3 (relative, |x| >= 1), the fp32 bars."""
     preset, make, _ = SAMPLES[tag]

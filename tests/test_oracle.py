@@ -96,17 +96,19 @@ def test_oracle_matches_reference_full_size(tag):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("tag,preset,make", [("c3_full", "large", wl.c3), ("c4_full", "base", wl.c4)])
+@pytest.mark.parametrize("tag,preset,make", [("c3_full", "large", wl.c3), ("c4_full", "base", wl.c4),
+                                             ("c5_full", "large1024", wl.c5)])
 def test_oracle_matches_reference_whole_batches(tag, preset, make):
-    """Every question of the b32 x s512 (ModernBERT-large) and b16 x s1024 (mmBERT-base) batches,
-    one question per forward as the engine packs them, against the logits and act logits the
-    reference's fp32 DecisionModel gave on the padded batch (tests/golden/<tag>/drift.npz)."""
+    """Every question of the b32 x s512 (ModernBERT-large), b16 x s1024 (mmBERT-base) and
+    b64 varlen (ModernBERT-large at 1024 positions) batches, one question per forward as the
+    engine packs them (no padding), against the logits and act logits the reference's fp32
+    DecisionModel gave on the padded batch (tests/golden/<tag>/drift.npz)."""
     g = np.load(os.path.join(GOLDEN, tag, "drift.npz"))
     b = make(0)
     assert list(g["lens"]) == list(b.lens)
     cfg = ck.PRESETS[preset]
     W = om.Weights(ck.generate_weights(cfg, 0))
-    lo, ac = om.run_batch(W, cfg, b)
+    lo, ac = om.run_per_question(W, cfg, b)
     ref = np.concatenate([g["logits"][i, :b.nmark[i]] for i in range(b.B)])
     assert np.abs(lo - ref).max() < 1e-5
     assert np.abs(ac.reshape(b.B, -1) - g["act_logits"]).max() < 1e-5
