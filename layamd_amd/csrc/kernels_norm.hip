@@ -317,6 +317,12 @@ void launch_fill_pattern(T* p, size_t n, uint32_t seed, hipStream_t st) {
 template void launch_fill_pattern<float>(float*, size_t, uint32_t, hipStream_t);
 template void launch_fill_pattern<bf16_t>(bf16_t*, size_t, uint32_t, hipStream_t);
 
+// Lane-strided dot products (scorer tail, act head): a lane's columns c = lane + 64 k are loaded
+// kDotBatch at a time, all of a batch's loads in flight together (one memory round trip per batch
+// instead of one per column), and accumulated in ascending k, as a plain loop would: the same
+// bits, in 12 instead of 17 us for the act head.
+constexpr int kDotBatch = 8;
+
 __global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, const int* __restrict__ rows,
                                                      float* __restrict__ xg, int R, int D) {
   const int lane = threadIdx.x & 63;
@@ -341,7 +347,18 @@ __global__ __launch_bounds__(256) void k_row_dot(const T* __restrict__ h, int ld
   if (r >= R) return;
   const T* hr = h + (size_t)r * ldh;
   float s = 0.f;
-  for (int c = lane; c < D; c += 64) s += Elt<T>::ld(hr + c) * w[c];
+  for (int c0 = lane; c0 < D; c0 += 64 * kDotBatch) {
+    float hv[kDotBatch], wv[kDotBatch];
+#pragma unroll
+    for (int k = 0; k < kDotBatch; k++) {
+      const int c = c0 + 64 * k;
+      hv[k] = c < D ? Elt<T>::ld(hr + c) : 0.f;
+      wv[k] = c < D ? w[c] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kDotBatch; k++)
+      if (c0 + 64 * k < D) s += hv[k] * wv[k];
+  }
   s = wave_sum(s);
   if (lane == 0) logits[r] = s + b[0];
 }
@@ -370,11 +387,32 @@ __global__ __launch_bounds__(256) void k_act_hidden(const float* __restrict__ cl
   const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const float* c = cls + (size_t)b * D;
   const int j0 = blockIdx.y * 16 + wv * 4;
-  float a[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int i = lane; i < D; i += 64) {
-    const float ci = c[i];
+  // the feature columns' weights and the biases do not depend on anything: loaded first
+  float wf[4], b0[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) a[u] += W0[(size_t)(j0 + u) * (D + 4) + i] * ci;
+  for (int u = 0; u < 4; u++) {
+    wf[u] = lane < 4 ? W0[(size_t)(j0 + u) * (D + 4) + D + lane] : 0.f;
+    b0[u] = B0[j0 + u];
+  }
+  // W0 . cls: each lane's columns i = lane + 64 k in ascending k, loaded kDotBatch columns at a time
+  // (all loads of a batch in flight together, instead of one round trip per column), accumulated in
+  // the same order
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = lane; i0 < D; i0 += 64 * kDotBatch) {
+    float cv[kDotBatch], wv_[4][kDotBatch];
+#pragma unroll
+    for (int k = 0; k < kDotBatch; k++) {
+      const int i = i0 + 64 * k;
+      cv[k] = i < D ? c[i] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; u++) wv_[u][k] = i < D ? W0[(size_t)(j0 + u) * (D + 4) + i] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kDotBatch; k++)
+      if (i0 + 64 * k < D) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) a[u] += wv_[u][k] * cv[k];
+      }
   }
 
   const float* z = logits + moff[b];
@@ -422,9 +460,9 @@ __global__ __launch_bounds__(256) void k_act_hidden(const float* __restrict__ cl
   for (int u = 0; u < 4; u++) {
     const int j = j0 + u;
     float v = a[u];
-    if (lane < 4) v += W0[(size_t)j * (D + 4) + D + lane] * feat;
+    if (lane < 4) v += wf[u] * feat;
     v = wave_sum(v);
-    if (lane == 0) hidden[(size_t)b * 256 + j] = gelu_erf(v + B0[j]);
+    if (lane == 0) hidden[(size_t)b * 256 + j] = gelu_erf(v + b0[u]);
   }
 }
 
