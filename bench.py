@@ -48,7 +48,8 @@ TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of bench.py --
                   "recorded in profiles/c3_geglu_gemm_hbm_traffic.md for GEMM sources with hash %s (the sources "
                   "benched here)")
 # the sources that decide the GEMM kernel's memory traffic
-GEMM_SOURCES = [os.path.join(REPO, "layamd_amd", "csrc", f) for f in ("kernels_gemm.hip", "kernels.h", "common.h")]
+GEMM_SOURCES = [os.path.join(REPO, "layamd_amd", "csrc", f)
+                for f in ("kernels_gemm.hip", "gemm_xl_tile.inc", "kernels.h", "common.h")]
 
 
 def gemm_source_hash():
@@ -220,8 +221,12 @@ def main():
            "LAYA_PROFILE": None}
     if a.pmc_probe:
         # counter runs serialize every dispatch, so tile timing is meaningless there: pin the plan the
-        # tuner picks for the dominant stage at this workload (192x128 tiles, one launch)
-        env.update({"LAYA_GEMM_CFG": 7})
+        # tuner picks for the dominant stage at this workload: 192x128 tiles (two per CU) over the rows
+        # that fill whole rounds of the 2 x 256 slots, 128x64 tiles over the rest, in one launch
+        rows = -(-int(sum(-(-int(L) // 8) * 8 for L in batch.lens)) // 64) * 64
+        tn = -(-2 * cfg.intermediate // 128)            # Wi: both GeGLU halves
+        split = -(-rows // 192) * tn // 512 * 512 // tn * 192
+        env.update({"LAYA_GEMM_CFG": 7, "LAYA_GEMM_SPLIT": "%d,8" % split} if 0 < split < rows else {"LAYA_GEMM_CFG": 7})
     eng = le.Engine(None, mdir, precision=precision, env=env)
     flat = batch.flat()
     if a.pmc_probe:

@@ -99,7 +99,7 @@ def build_probes(verbose: bool = True) -> None:
 
 def build(jobs: int = 8, force: bool = True, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + \
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".h", ".inc"))] + \
               [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
     steps = []
     for s in HIP_SOURCES:

@@ -703,6 +703,16 @@ struct Engine : EngineIface {
           if (gemm_split_valid(epi, g, c1, kb * bm, c2)) cands.push_back(TilePlan{c1, kb, c2});
       }
     }
+    // GeGLU: 192x128 tiles (two per CU) over the rows that fill whole rounds of the CUs' slots, and
+    // 128x64 or 128x128 tiles over the rest in the same launch, filling the slots that the partial
+    // last round of 192x128 tiles would leave idle
+    if (epi == EPI_GEGLU && !g.ln_mr && gemm_config_valid(epi, g, 7)) {
+      const int tn = (g.N + 127) / 128, slots = 2 * n_cu;
+      const int kb = ((g.M + 191) / 192) * tn / slots * slots / tn;
+      if (kb >= 1 && kb * 192 < g.M)
+        for (int c2 : {8, 3})
+          if (gemm_split_valid(epi, g, 7, kb * 192, c2)) cands.push_back(TilePlan{7, kb, c2});
+    }
     launch_fill_pattern((T*)const_cast<void*>(g.A), (size_t)g.M * g.lda, 0x9E3779B9u ^ (uint32_t)g.K, stream);
     hipEvent_t a, b;
     LAYA_HIP(hipEventCreate(&a));

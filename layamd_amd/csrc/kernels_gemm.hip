@@ -714,721 +714,47 @@ __device__ __forceinline__ void xl_k_loop64d(f32x16_t (&acc)[FM][FN], const u32x
 // one workgroup per CU): four stage buffers, two stages of lead.
 // LNX: the LayerNorm fold of GemmArgs.  With EPI_RESID the kernel writes Xh and the per-group
 // statistics; with EPI_STORE, EPI_QKV and EPI_GEGLU it applies the fold to its product.
+// LDS of one tile (16-byte chunks): the K stages (two whole stages; LOOP 1: three A buffers and two
+// W buffers; LOOP 2: four whole stages) and, for the QKV projection with two stages where it fits,
+// the RoPE tables of the tile's rows
+template <int BM, int BN, int EPI, int LOOP>
+struct XlLds {
+  static constexpr int BMQ = (BM + 31) / 32 * 32;
+  static constexpr int SA = BMQ * 8, SW = BN * 8;
+  static constexpr int NST = LOOP == 1 ? 3 * SA + 2 * SW : LOOP == 2 ? 4 * (SA + SW) : 2 * (SA + SW);
+  static constexpr bool PRE = EPI == EPI_QKV && LOOP == 0 && (NST + BM * 16) * 16 < 160 * 1024;
+  static constexpr int chunks = NST + (PRE ? BM * 16 : 0);
+};
+
+// One BM x BN output tile (tile `bid` of the GEMM; with EPI_PARTIAL, bid also selects the K chunk),
+// computed by the 256 threads of the calling workgroup in the LDS array L (XlLds chunks)
+template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP, bool LNX>
+__device__ __forceinline__ void xl_tile(const GemmArgs a, int bid0, u32x4_t* L) {
+#include "gemm_xl_tile.inc"
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP, bool LNX>
 __global__ __launch_bounds__(256, 1) void k_gemm_xl(const GemmArgs a) {
-  using T = bf16_t;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  // the A part of a stage holds BM rounded up to whole DMA instructions (32 rows over the 4 waves)
-  constexpr int BMQ = (BM + 31) / 32 * 32;
-  constexpr int PA = BMQ / 32, PB = BN / 32;             // DMA instructions per wave and stage
-  static_assert(WM * WN == 4 && WTM % 32 == 0 && WTN % 64 == 0 && BN % 64 == 0, "tile");
-  static_assert(PB % 2 == 0, "swizzle parity of the W part: even instruction count per wave");
-  // K stages: two whole stages (A then W part), or (RING) three A buffers and two W buffers (BMQ and
-  // BN rows of 128 bytes); after the K loop the same memory holds the epilogue's staging area (SB
-  // bytes per wave) and, for the QKV projection, the RoPE tables of the tile's rows
-  static_assert(LOOP == 0 || BM * BN <= 128 * 128, "the ring and deep loops are for 128x128 tiles");
-  constexpr bool RING = LOOP == 1;
-  constexpr int NBD = 4;                                 // stage buffers of the deep loop
-  constexpr int SA = BMQ * 8, SW = BN * 8;               // buffer sizes in 16-byte chunks
-  struct Stage64 { u32x4_t a[SA]; u32x4_t b[SW]; };
-  constexpr int NST = RING ? 3 * SA + 2 * SW : LOOP == 2 ? NBD * (SA + SW) : 2 * (SA + SW);
-  // QKV projection (two K buffers): the RoPE tables of the tile's rows ([BM][32] floats of cos,
-  // then of sin) get LDS of their own where it fits, and are fetched during the K loop
-  constexpr bool PRE = EPI == EPI_QKV && LOOP == 0 && (NST + BM * 16) * 16 < 160 * 1024;
-  __shared__ u32x4_t L[NST + (PRE ? BM * 16 : 0)];
-  constexpr int BMP = (BM + 63) / 64 * 64;
-  // staging bytes per wave: at least a block of 32 rows x 32 fp32 columns, so every epilogue
-  // stages whole 32-column accumulator blocks
-  constexpr int SB = (BMP + BN) * 16 > 32 * 32 * 4 ? (BMP + BN) * 16 : 32 * 32 * 4;
-  static_assert(4 * SB + (EPI == EPI_QKV && !PRE ? 2 * BM * 32 * 4 : 0) + (LNX ? BN * 4 : 0) +
-                    (LNX && EPI == EPI_QKV ? 2 * BMP * 4 : 0) <= NST * 16,
-                "epilogue LDS");
-  static_assert(EPI != EPI_QKV || BM * 8 % 256 == 0, "RoPE table pieces: whole rounds of the workgroup");
+  __shared__ u32x4_t L[XlLds<BM, BN, EPI, LOOP>::chunks];
+  const int bid0 = blockIdx.x;
+#include "gemm_xl_tile.inc"
+}
 
-#ifdef LAYA_TILE_TRACE
-  TileTrace tt;
-  tt.start();
-  unsigned long long& twait = tt.w;
-#else
-  unsigned long long twait = 0;
-  (void)twait;
-#endif
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hi = lane >> 5;
-  const int tilesN = (a.N + BN - 1) / BN, tilesM = (a.M + BM - 1) / BM;
-  // split-K partials: workgroup split * tiles + t computes tile t over K chunk `split` (a.K deep)
-  int bid = blockIdx.x, split = 0;
-  if constexpr (EPI == EPI_PARTIAL) {
-    split = bid / (tilesM * tilesN);
-    bid -= split * tilesM * tilesN;
-  }
-  int tm, tn;
-  tile_coords(bid, tilesM, tilesN, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int D = a.H * a.HD;
-  // all tiles use the transposed product except the V columns of the QKV projection, which are
-  // stored transposed themselves (V^T) and keep the direct one
-  const bool swap = EPI == EPI_QKV ? n0 < 2 * D : true;
-
-  // RoPE positions of the rows whose table pieces this thread stages in the QKV epilogue, loaded
-  // first so that they are the oldest loads (the K loop's counted waits then never wait on them)
-  // and the epilogue can issue its table loads at once
-  constexpr int NT = BM * 8 / 256;
-  constexpr int NTX = PRE ? 2 * NT : 0;                  // RoPE table fills issued after stage 1's A part
-  // Loaded without a branch, through a buffer resource that has no records when the tile needs no
-  // tables (the loads then read 0 and touch no memory): loads in a conditional block make the
-  // compiler wait for them where the block ends, before the K stages are even requested.
-  int pp[EPI == EPI_QKV ? NT : 1];
-  if constexpr (EPI == EPI_QKV) {
-    const bool need = swap && a.rope_cos != nullptr;
-    const __amdgpu_buffer_rsrc_t rpos =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(a.pos), (short)0, need ? a.M * 4 : 0, 0x00020000);
-#pragma unroll
-    for (int k = 0; k < NT; k++)
-      pp[k] = __builtin_amdgcn_raw_buffer_load_b32(rpos, min(m0 + ((tid + 256 * k) >> 3), a.M - 1) * 4, 0, 0);
-  }
-
-  // LayerNorm fold, consumer side: the mean and rstd of this lane's FM rows and the column sum of
-  // column n0 + tid, loaded before the first K stage is requested (the K loop's first wait then
-  // covers them: loads complete in order) and kept in registers until the epilogue
-  constexpr bool LNC = LNX && (EPI == EPI_STORE || EPI == EPI_QKV || EPI == EPI_GEGLU);
-  constexpr bool LNP = LNX && EPI == EPI_RESID;
-  static_assert(BN <= 256, "one column sum per thread");
-  float lnm[LNC ? FM : 1], lnr[LNC ? FM : 1];            // mean and rstd of rows wm WTM + 32 i + l32
-  float lnc_pre = 0.f;                                    // column sum n0 + tid (tid < BN)
-  if constexpr (LNC) {
-    // rows past M read 0
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ln_mr), (short)0,
-                                                                       a.M * 8, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (m0 + wm * WTM + 32 * i + l32) * 8, 0, 0);
-      lnm[i] = __uint_as_float(v[0]);
-      lnr[i] = __uint_as_float(v[1]);
-    }
-    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ln_c), (short)0,
-                                                                       (n0 + BN <= a.N ? n0 + BN : a.N) * 4, 0x00020000);
-    lnc_pre = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, (n0 + (tid < BN ? tid : 0)) * 4, 0, 0));
-  }
-
-  XlDma64<PA, PB> dm;
-  const size_t k0 = (size_t)split * a.K;                 // first K column of this workgroup
-  dm.rA = make_rsrc(reinterpret_cast<const T*>(a.A) + k0, (uint32_t)(((size_t)a.M * a.lda - k0) * sizeof(T)));
-  dm.rB = make_rsrc(reinterpret_cast<const T*>(a.W) + k0, (uint32_t)(((size_t)a.N * a.ldw - k0) * sizeof(T)));
-  dm.rNone = make_rsrc(a.A, 0u);           // zero length: every offset out of range
-  const int lda_b = a.lda * (int)sizeof(T), ldw_b = a.ldw * (int)sizeof(T);
-  // instruction o of this wave fills rows 8 (wave PA + o) ..: the swizzle's row term is the parity
-  // of wave PA + o (PA may be odd)
-  dm.va[0] = dma64_voff(m0, wave * PA * 8, lda_b, lane, (wave * PA) & 1);
-  dm.va[1] = dma64_voff(m0, wave * PA * 8, lda_b, lane, ((wave * PA) & 1) ^ 1);
-  dm.vb[0] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 0);
-  dm.vb[1] = dma64_voff(n0, wave * PB * 8, ldw_b, lane, 1);
-  dm.wsa = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PA * 1024);
-  dm.wsb = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * (uint32_t)(PB * 1024);
-  dm.lda8 = 8 * lda_b;
-  dm.ldw8 = 8 * ldw_b;
-  // 32-deep slices of this workgroup's K (a split-K chunk: the last one may be shorter)
-  dm.ns = (EPI == EPI_PARTIAL && a.kfull > 0 ? min(a.K, a.kfull - (int)k0) : a.K) / 32;
-  Stage64& T0 = *reinterpret_cast<Stage64*>(L);
-  Stage64& T1 = *reinterpret_cast<Stage64*>(L + SA + SW);
-  if constexpr (LOOP == 2) {
-    // stages 0 .. NBD - 2 into buffers 0 .. NBD - 2
-#pragma unroll
-    for (int g = 0; g < NBD - 1; g++) {
-      const uint32_t lg = lds_addr(L) + (uint32_t)(g * (SA + SW) * 16);
-#pragma unroll
-      for (int o = 0; o < PA; o++) dm.op_a(o, lg, g);
-#pragma unroll
-      for (int o = 0; o < PB; o++) dm.op_b(o, lg + SA * 16, g);
-    }
-  } else if constexpr (!RING) {
-    // stage 0, then the A part of stage 1 (the K loop's first sub-step issues its W part)
-#pragma unroll
-    for (int o = 0; o < PA; o++) dm.op_a(o, lds_addr(T0.a), 0);
-#pragma unroll
-    for (int o = 0; o < PB; o++) dm.op_b(o, lds_addr(T0.b), 0);
-#pragma unroll
-    for (int o = 0; o < PA; o++) dm.op_a(o, lds_addr(T1.a), 1);
-    if constexpr (PRE) {
-      // RoPE table rows: piece k of this thread is row r = (tid + 256 k) / 8, 16-byte chunk tid % 8,
-      // so one DMA instruction of wave w fills rows 32 k + 8 w .. + 7, i.e. LDS bytes
-      // (4 k + w) * 1024 on; the K loop's first wait leaves these in flight, its second covers them
-      // Issued by every tile, without a branch (a tile that needs no tables reads through
-      // resources without records: nothing is read, and the K loop's first wait count holds).
-      // The table resources do not bound the rows: positions come from the host's packing, which
-      // keeps them below the tables' row count (the length limit plus the padding rows).
-      const bool need = swap && a.rope_cos != nullptr;
-      const u32x4_t rc = need ? make_rsrc(a.rope_cos, 0xFFFFFFF0u) : dm.rNone;
-      const u32x4_t rs = need ? make_rsrc(a.rope_sin, 0xFFFFFFF0u) : dm.rNone;
-      const uint32_t tc = lds_addr(L + NST), ts = tc + BM * 128;
-      const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
-      // All offsets first, each pinned by an empty statement that uses it: the compiler's waits for
-      // the position loads (which in hardware also wait for every fill issued after them) then
-      // come together here, not between table fills, where each would wait for the fills before it.
-      // (LDS slot lane % 8 of table row r holds the row's 16-byte chunk (lane % 8) ^ rope_sw(r))
-      uint32_t voff[NT];
-#pragma unroll
-      for (int k = 0; k < NT; k++) {
-        voff[k] = (uint32_t)pp[k] * 128u + (uint32_t)((lane & 7) ^ rope_sw((tid + 256 * k) >> 3)) * 16u;
-        asm volatile("" ::"v"(voff[k]));
-      }
-#pragma unroll
-      for (int k = 0; k < NT; k++) {
-        dma16(rc, tc + (4u * k + w) * 1024u, voff[k], 0u);
-        dma16(rs, ts + (4u * k + w) * 1024u, voff[k], 0u);
-      }
-    }
-  } else {
-    const uint32_t l0 = lds_addr(L);
-#pragma unroll
-    for (int o = 0; o < PB; o++) dm.op_b(o, l0 + 3 * SA * 16, 0);
-#pragma unroll
-    for (int o = 0; o < PA; o++) dm.op_a(o, l0, 0);
-#pragma unroll
-    for (int o = 0; o < PB; o++) dm.op_b(o, l0 + (3 * SA + SW) * 16, 1);
-#pragma unroll
-    for (int o = 0; o < PA; o++) dm.op_a(o, l0 + SA * 16, 1);
-#pragma unroll
-    for (int o = 0; o < PA; o++) dm.op_a(o, l0 + 2 * SA * 16, 2);
-  }
-
-  // Output coordinates.  Transposed product: lane holds, for block (i, j) and element e, output row
-  // rbase + 32 i + lane % 32 and columns cbase + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4, i.e. four
-  // consecutive columns per e / 4.  Direct product: rows rbase + 32 i + 8 (e / 4) + 4 (lane / 32) +
-  // e % 4 (four consecutive rows per e / 4) and column cbase + 32 j + lane % 32.
-  const int rbase = m0 + wm * WTM, cbase = n0 + wn * WTN;
-  f32x16_t acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
-  // The residual update X += A W^T + b adds X to the finished product, (A W^T + X) + b, in the
-  // accumulator layout: block (i, j) of the lane's X is four 16-byte loads of 4 columns (rows past
-  // M read 0, columns past N are never stored).  Where does X wait in registers?
-  //   XIN: tiles alone on their CU with the two-buffer loop and room for a second register copy of
-  //        the accumulators: the K loop's first FM FN stages each issue one block (the HBM reads
-  //        spread over the loop instead of holding up its first stage);
-  //   XPRE: other tiles with room for the copy: all of it before the K loop, one wait;
-  //   otherwise (XEPI) the epilogue loads each block row as it comes to it, or, for tiles alone
-  //        on their CU, a block row ahead (two workgroups on a CU cover each other's waits).
-  // The sum and its order are the same in all three.
-  constexpr bool XRES = EPI == EPI_RESID;
-  constexpr bool ONE_PER_CU = NST * 16 > 80 * 1024;
-  // XFL (every residual kernel but the LayerNorm-fold producers, which need the updated values in
-  // the accumulator layout for their statistics): X is read in the epilogue's flush order, 16 bytes
-  // per lane along each staged row, so one load instruction covers eight whole 128-byte row
-  // segments, and added to the staged product as it is stored.  The accumulator-layout loads of the
-  // other placements touch 32 rows per instruction, 32 bytes of each, and re-request every line four
-  // times; issued during the K loop they slowed it by a quarter.  Each staged block's X is loaded
-  // one block ahead, the first block's during the K loop's last stage.
-  constexpr bool XFL = XRES && !LNX;
-  constexpr bool XIN = XRES && !XFL && LOOP == 0 && ONE_PER_CU && FM * FN * 16 <= 160;
-  constexpr bool XPRE = XRES && !XFL && !XIN && FM * FN * 16 <= 64;
-  constexpr bool XEPI = XRES && !XFL && !XIN && !XPRE;
-  f32x4_t xr[XIN || XPRE ? FM : 1][XIN || XPRE ? FN : 1][4];
-  const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
-      XRES ? a.X : nullptr, (short)0, XRES ? (int)((size_t)a.M * a.ldx * sizeof(float)) : 0, 0x00020000);
-  // XFL: the residual epilogue stages 32 rows x XCW fp32 columns per block (XCPR 16-byte chunks per
-  // row); lane item lane + 64 it of a block is row item / XCPR, chunk item % XCPR
-  constexpr int XCW = xl_fitw(WTN, SB / 128), XCPR = XCW / 4, XNIT = 32 * XCPR / 64, XNB = FM * (WTN / XCW);
-  // XFLK: tiles alone on their CU with the two-buffer loop and room for all of X in registers: the
-  // K loop's first XNB stages each issue one block's loads (piece p = block p), so X is read while
-  // the MFMAs run instead of at the end, where every tile of a one-round launch would read it at
-  // once.  Other XFL tiles load each block one block ahead in the epilogue (the first one during
-  // the K loop's last stage).
-  constexpr bool XFLK = XFL && LOOP == 0 && ONE_PER_CU && XNB * XNIT * 4 <= 160;
-  f32x4_t xall[XFLK ? XNB : 1][XFL ? XNIT : 1];
-  f32x4_t xq[XFL && !XFLK ? 2 : 1][XFL ? XNIT : 1];
-  // X of staged block kb (block row kb / (WTN / XCW), column part kb % (WTN / XCW)) into xv
-  auto xfl_load = [&](f32x4_t (&xv)[XFL ? XNIT : 1], int kb) {
-    if constexpr (XFL) {
-      const int i = kb / (WTN / XCW), c0 = cbase + (kb % (WTN / XCW)) * XCW;
-#pragma unroll
-      for (int it = 0; it < XNIT; it++) {
-        const int item = lane + 64 * it, r = item / XCPR, q = item % XCPR;
-        const uint32_t off = ((uint32_t)(rbase + i * 32 + r) * (uint32_t)a.ldx + (uint32_t)(c0 + 4 * q)) * 4u;
-        xv[it] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
-      }
-    }
-  };
-  // X at rows rbase + 32 i + lane % 32, columns cbase + 32 j + 8 g + 4 hi .. + 3
-  auto xload = [&](int i, int j, int g) -> f32x4_t {
-    const uint32_t off = ((uint32_t)(rbase + i * 32 + l32) * (uint32_t)a.ldx + (uint32_t)(cbase + j * 32 + 8 * g + 4 * hi)) * 4u;
-    // reinterpret the whole 16 bytes as floats (a bit_cast of one vector component is miscompiled
-    // by this compiler: it reads component 0)
-    return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rX, (int)off, 0, 0));
-  };
-  // piece p of XIN: block (p / FN, p % FN)
-  auto xpiece = [&](auto p) {
-    if constexpr (XIN) {
-      constexpr int i = decltype(p)::value / FN, j = decltype(p)::value % FN;
-#pragma unroll
-      for (int g = 0; g < 4; g++) xr[i][j][g] = xload(i, j, g);
-    }
-  };
-  if constexpr (XPRE) {
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) xr[i][j][g] = xload(i, j, g);
-    // Wait for these loads once, here, with a wait the compiler sees (not inline assembly).  Left to
-    // itself it would wait where the epilogue reads them, and its wait analysis, which merges the
-    // loop entry into every iteration, could repeat such waits inside the K loop, where they would
-    // wait for the next stage's DMA fills instead.  These loads come after the prologue fills, so
-    // this wait covers those too.
-    __builtin_amdgcn_s_waitcnt(0x0F70);                   // vmcnt(0); expcnt, lgkmcnt: no wait
-  }
-
-  const int arow = wm * WTM + l32, brow = wn * WTN + l32;
-  const int sw = (lane & 7) ^ ((lane >> 3) & 1);          // g(row) of fragment rows 32 n + lane % 32
-  LAYA_TT_MARK(t1);
-
-  if constexpr (RING) {
-    if (swap) xl_k_loop64r<true, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
-    else xl_k_loop64r<false, FM, FN, PA, PB, SA, SW>(acc, L, dm, arow, brow, hi, sw);
-  } else if constexpr (LOOP == 2) {
-    if (swap) xl_k_loop64d<true, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
-    else xl_k_loop64d<false, FM, FN, PA, PB, SA, SW, NBD>(acc, L, dm, arow, brow, hi, sw);
-  } else {
-    if constexpr (XIN) {
-      if (swap) xl_k_loop64<true, NTX, FM * FN, 4, 0>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, [] {}, twait);
-      else xl_k_loop64<false, NTX, FM * FN, 4, 0>(acc, T0, T1, dm, arow, brow, hi, sw, xpiece, [] {}, twait);
-    } else if constexpr (XFLK) {
-      auto piece = [&](auto p) { xfl_load(xall[decltype(p)::value], decltype(p)::value); };
-      if (swap) xl_k_loop64<true, NTX, XNB, XNIT, 0>(acc, T0, T1, dm, arow, brow, hi, sw, piece, [] {}, twait);
-      else xl_k_loop64<false, NTX, XNB, XNIT, 0>(acc, T0, T1, dm, arow, brow, hi, sw, piece, [] {}, twait);
-    } else if constexpr (XFL) {
-      auto none = [](auto) {};
-      auto first = [&] { xfl_load(xq[0], 0); };
-      if (swap) xl_k_loop64<true, NTX, 0, 0, XNIT>(acc, T0, T1, dm, arow, brow, hi, sw, none, first, twait);
-      else xl_k_loop64<false, NTX, 0, 0, XNIT>(acc, T0, T1, dm, arow, brow, hi, sw, none, first, twait);
-    } else {
-      auto none = [](auto) {};
-      if (swap) xl_k_loop64<true, NTX, 0, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, [] {}, twait);
-      else xl_k_loop64<false, NTX, 0, 0, 0>(acc, T0, T1, dm, arow, brow, hi, sw, none, [] {}, twait);
-    }
-  }
-  LAYA_TT_MARK(t2);
-  if constexpr (XFLK) {
-    // Every X piece has landed by now (issued in the first stages; the loop's own waits, which the
-    // compiler does not see, covered them).  Saying so with a wait it sees keeps it from waiting on
-    // them in the flush, where each such wait would also hold every store issued before it.
-    __builtin_amdgcn_s_waitcnt(0x0F70);                   // vmcnt(0); expcnt, lgkmcnt: no wait
-  }
-
-  // ---------------- epilogue ----------------
-  // The tile leaves through LDS, one 32-row block (or column part of it) at a time: each wave
-  // writes the block (bias, activation, GeGLU, RoPE applied in registers) into its quarter of the
-  // staging area as rows of 16-byte chunks, swizzled by row, then streams whole rows out with
-  // 16-byte stores (full cache lines).  The K stages hold the RoPE tables for the QKV projection.
-  // Global loads are issued before the first store (on gfx9 vmcnt counts stores too, so a load
-  // issued after a store would wait for it), except the XEPI residual loads, each issued a block
-  // row ahead of its use.
-  __syncthreads();                                        // every wave is done with the K stages
-  char* stg = reinterpret_cast<char*>(L) + wave * SB;
-  auto sync_wave = [] {                                   // this wave's LDS writes are visible to it
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_wave_barrier();
-  };
-  // byte offset of 16-byte chunk q of staged row r (cpr chunks per row, a power of two).  The chunk
-  // is XORed with the row's index among the rows that share one pass over the 64 banks (256 bytes:
-  // 16 / cpr rows for short rows), so that the 32 rows a column of lanes writes at once spread over
-  // every chunk position of their bank range (8-byte writes: 2-way at most; 16-byte: none), while a
-  // flush pass, 16 lanes over whole rows that share that index, stays conflict-free.
-  auto sidx = [](int r, int q, int cpr) {
-    const unsigned rpl = cpr >= 16 ? 1u : 16u / (unsigned)cpr;
-    return (r * cpr + (q ^ (int)(((unsigned)r / rpl) & (unsigned)(cpr - 1)))) * 16;
-  };
-  // four bf16 values at staged row r, columns c..c+3 (c % 4 == 0)
-  auto put8 = [&](int r, int c, int cpr, float v0, float v1, float v2, float v3) {
-    uint2 u;
-    u.x = pk_bf16(v0, v1);
-    u.y = pk_bf16(v2, v3);
-    *reinterpret_cast<uint2*>(stg + sidx(r, c >> 3, cpr) + ((c >> 2) & 1) * 8) = u;
-  };
-  // streams 32 staged rows of cpr chunks: row r goes to row_ptr(r) (null: skipped), chunks q < nq
-  auto flush = [&](int cpr, auto&& row_ptr, int nq) {
-    sync_wave();
-#pragma unroll
-    for (int it = 0; it < 32 * cpr / 64; it++) {
-      const int item = lane + 64 * it, r = item / cpr, q = item % cpr;
-      char* p = row_ptr(r);
-      if (p != nullptr && q < nq)
-        *reinterpret_cast<u32x4_t*>(p + q * 16) = *reinterpret_cast<const u32x4_t*>(stg + sidx(r, q, cpr));
-    }
-    sync_wave();
-  };
-  auto bias4 = [&](int n) -> float4 {
-    return (a.bias && n < a.N) ? *reinterpret_cast<const float4*>(a.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  // LayerNorm fold: the tile's BN column sums, staged at the end of the stage memory (past the
-  // staging area and the RoPE tables); the fold r (acc - m c) is applied to each accumulator where
-  // the epilogue reads it, before bias and activation
-  float* const lcs = reinterpret_cast<float*>(L) + NST * 4 - BN;
-  // and, below them (QKV projection), the tile rows' means and rstds, which the V^T epilogue reads
-  // by row groups that differ from the accumulator layout's
-  float* const lrm = lcs - 2 * BMP;
-  if constexpr (LNC) {
-    if (tid < BN) lcs[tid] = lnc_pre;
-    if constexpr (EPI == EPI_QKV) {
-      if (wn == 0 && !hi)
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-          lrm[wm * WTM + 32 * i + l32] = lnm[i];
-          lrm[BMP + wm * WTM + 32 * i + l32] = lnr[i];
-        }
-    }
-    __syncthreads();
-  }
-  // r (acc - m c) of an accumulator of row block i
-  auto lnt = [&](float v, float c, int i) {
-    if constexpr (LNC) return __fmul_rn(fmaf(-lnm[i], c, v), lnr[i]);
-    else return v;
-  };
-  // elements 4 g .. 4 g + 3 of block (i, j) of the transposed product (row 32 i + lane % 32,
-  // columns 32 j + 8 g + 4 hi ..), fold applied
-  auto av4 = [&](int i, int j, int g) -> float4 {
-    if constexpr (LNC) {
-      const float4 c = *reinterpret_cast<const float4*>(lcs + cbase - n0 + j * 32 + 8 * g + 4 * hi);
-      return make_float4(lnt(acc[i][j][4 * g + 0], c.x, i), lnt(acc[i][j][4 * g + 1], c.y, i),
-                         lnt(acc[i][j][4 * g + 2], c.z, i), lnt(acc[i][j][4 * g + 3], c.w, i));
-    } else {
-      return make_float4(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-    }
-  };
-  auto nchunks = [](int valid_elems, int per_chunk, int cpr) { return max(0, min(cpr, (valid_elems + per_chunk - 1) / per_chunk)); };
-  // widest power-of-two column count <= cap that divides w
-  constexpr auto fitw = [](int w, int cap) { int c = w & -w; while (c > cap) c /= 2; return c; };
-
-  // the bias loads and adds exist only in the kernels for GEMMs that have a bias (HB)
-  auto ab = [](float v, float b) {
-    if constexpr (HB) return v + b;
-    else return v;
-  };
-  if constexpr (EPI == EPI_RESID || EPI == EPI_PARTIAL) {
-    // fp32: blocks of 32 rows x CW columns (split-K partials go to their chunk's slice of X)
-    float* const xo = EPI == EPI_PARTIAL ? a.X + (size_t)split * a.M * a.ldx : a.X;
-    constexpr int CW = fitw(WTN, SB / 128), CPR = CW / 4;
-    static_assert(CW % 32 == 0, "whole accumulator blocks per staged block");
-    static_assert(CW == XCW && CPR == XCPR, "XFL block geometry");
-    if constexpr (XFL && LOOP != 0) xfl_load(xq[0], 0);   // (the ring and deep loops have no tail hook)
-    float4 bb[FN][4] = {};
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) if constexpr (HB) bb[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
-    // LayerNorm statistics of the updated rows (LNP), per 64-column group = accumulator blocks
-    // j, j + 1 (j even): each lane takes its 16 values of a block (sum, then squared deviations
-    // from their mean), combines its two blocks and then its half of the group with lane l ^ 32's
-    // (lower half first) by Chan et al.'s pairwise update, M2 = M2a + M2b + (Sb - Sa)^2 nb / (na n).
-    // The values, their order and the arithmetic do not depend on the tile shape.
-    float ls0 = 0.f, lq0 = 0.f;                           // the lane's first block of a group
-    // XEPI: X of block row i (and i + 1 with XAHEAD), in xb[i % XB]
-    constexpr bool XAHEAD = XEPI && ONE_PER_CU;
-    constexpr int XB = XAHEAD ? 2 : 1;
-    f32x4_t xb[XB][XEPI ? FN : 1][4];
-    if constexpr (XAHEAD) {
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) xb[0][j][g] = xload(0, j, g);
-    }
-    // acc + X of block (i, j), elements 4 g .. 4 g + 3
-    auto accx = [&](int i, int j, int g) -> f32x4_t {
-      f32x4_t v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-      if constexpr (XRES && !XFL) {
-        f32x4_t x;
-        if constexpr (XEPI) x = xb[i % XB][j][g];
-        else x = xr[i][j][g];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = __fadd_rn(v[u], x[u]);
-      }
-      return v;
-    };
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-      if constexpr (XEPI) {
-        const int il = XAHEAD ? i + 1 : i;                // the block row to load
-        if (il < FM)
-#pragma unroll
-          for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) xb[il % XB][j][g] = xload(il, j, g);
-      }
-#pragma unroll
-      for (int cp = 0; cp < WTN / CW; cp++) {
-        const int kb = i * (WTN / CW) + cp;               // staged block index
-        if constexpr (XFL && !XFLK) {
-          if (kb + 1 < XNB) xfl_load(xq[(kb + 1) & 1], kb + 1);
-        }
-#pragma unroll
-        for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++) {
-          float v16[16];
-#pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const f32x4_t s4 = accx(i, j, g);
-            float4 v;
-            // (XFL stages the bare product: X, then the bias, are added in the flush)
-            v.x = XFL ? s4[0] : ab(s4[0], bb[j][g].x);
-            v.y = XFL ? s4[1] : ab(s4[1], bb[j][g].y);
-            v.z = XFL ? s4[2] : ab(s4[2], bb[j][g].z);
-            v.w = XFL ? s4[3] : ab(s4[3], bb[j][g].w);
-            *reinterpret_cast<float4*>(stg + sidx(l32, (j * 32 - cp * CW + 8 * g + 4 * hi) >> 2, CPR)) = v;
-            v16[4 * g + 0] = v.x; v16[4 * g + 1] = v.y; v16[4 * g + 2] = v.z; v16[4 * g + 3] = v.w;
-          }
-          if constexpr (LNP) {
-            float bs = 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++) bs = __fadd_rn(bs, v16[u]);
-            const float bm = __fmul_rn(bs, 0.0625f);
-            float bq = 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-              const float d = __fsub_rn(v16[u], bm);
-              bq = fmaf(d, d, bq);
-            }
-            if ((j & 1) == 0) {
-              ls0 = bs; lq0 = bq;
-            } else {
-              const float d1 = __fsub_rn(bs, ls0);
-              const float sl = __fadd_rn(ls0, bs), ql = fmaf(__fmul_rn(d1, d1), 0.03125f, __fadd_rn(lq0, bq));
-              const float so = __shfl_xor(sl, 32, 64), qo = __shfl_xor(ql, 32, 64);
-              const float slo = hi ? so : sl, shi = hi ? sl : so, qlo = hi ? qo : ql, qhi = hi ? ql : qo;
-              const float d2 = __fsub_rn(shi, slo);
-              const float m2 = fmaf(__fmul_rn(d2, d2), 0.015625f, __fadd_rn(qlo, qhi));
-              const int row = rbase + i * 32 + l32;
-              // (a tile may extend past N; N % 64 == 0, so a group lies wholly inside or outside)
-              if (!hi && row < a.M && cbase + 32 * (j - 1) < a.N)
-                *reinterpret_cast<float2*>(a.stats + ((size_t)((cbase + 32 * (j - 1)) / 64) * a.ldst + row) * 2) =
-                    make_float2(__fadd_rn(slo, shi), m2);
-            }
-          }
-        }
-        const int c0 = cbase + cp * CW;
-        if constexpr (XFL) {
-          // (staged + X) + bias, rounded as the other placements round it: X + product, then bias
-          const int nq = nchunks(a.N - c0, 4, CPR);
-          const f32x4_t(&xv)[XNIT] = XFLK ? xall[XFLK ? kb : 0] : xq[XFLK ? 0 : kb & 1];
-          sync_wave();
-#pragma unroll
-          for (int it = 0; it < XNIT; it++) {
-            const int item = lane + 64 * it, r = item / CPR, q = item % CPR;
-            const int m = rbase + i * 32 + r;
-            if (m < a.M && q < nq) {
-              const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + sidx(r, q, CPR));
-              float4 bq = make_float4(0.f, 0.f, 0.f, 0.f);
-              if constexpr (HB) bq = bias4(c0 + 4 * q);
-              f32x4_t o;
-              o[0] = ab(__fadd_rn(sv[0], xv[it][0]), bq.x);
-              o[1] = ab(__fadd_rn(sv[1], xv[it][1]), bq.y);
-              o[2] = ab(__fadd_rn(sv[2], xv[it][2]), bq.z);
-              o[3] = ab(__fadd_rn(sv[3], xv[it][3]), bq.w);
-              *reinterpret_cast<f32x4_t*>(xo + (size_t)m * a.ldx + c0 + 4 * q) = o;
-            }
-          }
-          sync_wave();
-        } else {
-          flush(CPR, [&](int r) -> char* {
-            const int m = rbase + i * 32 + r;
-            return m < a.M ? reinterpret_cast<char*>(xo + (size_t)m * a.ldx + c0) : nullptr;
-          }, nchunks(a.N - c0, 4, CPR));
-        }
-        if constexpr (LNP) {
-          // the same block again as bf16 (Xh, the next GEMM's A operand)
-          constexpr int CPH = CW / 8;
-#pragma unroll
-          for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const f32x4_t s4 = accx(i, j, g);
-              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPH, ab(s4[0], bb[j][g].x), ab(s4[1], bb[j][g].y),
-                   ab(s4[2], bb[j][g].z), ab(s4[3], bb[j][g].w));
-            }
-          flush(CPH, [&](int r) -> char* {
-            const int m = rbase + i * 32 + r;
-            return m < a.M ? reinterpret_cast<char*>(a.Xh + (size_t)m * a.ldxh + c0) : nullptr;
-          }, nchunks(a.N - c0, 8, CPH));
-        }
-      }
-    }
-  } else if constexpr (EPI == EPI_STORE || EPI == EPI_GEGLU) {
-    // bf16 rows of OW output columns, blocks of 32 rows x CW columns
-    constexpr int OW = EPI == EPI_GEGLU ? WTN / 2 : WTN;
-    constexpr int CW = fitw(OW, SB / 64), CPR = CW / 8;
-    static_assert(CW % 32 == 0, "whole accumulator blocks per staged block");
-    const int ocol = EPI == EPI_GEGLU ? cbase / 2 : cbase, ncol = EPI == EPI_GEGLU ? a.N / 2 : a.N;
-    // bias per (column block, e / 4): input and gate parts for GeGLU
-    float4 bx[FN][4] = {};
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) if constexpr (HB) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
-    auto f = [](float v) {
-      if constexpr (ACT == ACT_RELU) v = fmaxf(v, 0.f);
-      if constexpr (ACT == ACT_GELU) v = gelu_erf_as(v);
-      return v;
-    };
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int cp = 0; cp < OW / CW; cp++) {
-        if constexpr (EPI == EPI_STORE) {
-#pragma unroll
-          for (int j = cp * CW / 32; j < (cp + 1) * CW / 32; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const float4 v = av4(i, j, g);
-              put8(l32, j * 32 - cp * CW + 8 * g + 4 * hi, CPR, f(ab(v.x, bx[j][g].x)), f(ab(v.y, bx[j][g].y)),
-                   f(ab(v.z, bx[j][g].z)), f(ab(v.w, bx[j][g].w)));
-            }
-        } else {
-          // 64-column groups [input 32 | gate 32] (blocks jp, jp + 1) -> output column (c / 64) * 32 + c % 64
-#pragma unroll
-          for (int jp = cp * CW / 16; jp < (cp + 1) * CW / 16; jp += 2)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const float4 x = bx[jp][g], y = bx[jp + 1][g];
-              const float4 p = av4(i, jp, g), q = av4(i, jp + 1, g);
-              put8(l32, jp * 16 - cp * CW + 8 * g + 4 * hi, CPR, gelu_erf_as(ab(p.x, x.x)) * ab(q.x, y.x),
-                   gelu_erf_as(ab(p.y, x.y)) * ab(q.y, y.y), gelu_erf_as(ab(p.z, x.z)) * ab(q.z, y.z),
-                   gelu_erf_as(ab(p.w, x.w)) * ab(q.w, y.w));
-            }
-        }
-        const int c0 = ocol + cp * CW;
-        flush(CPR, [&](int r) -> char* {
-          const int m = rbase + i * 32 + r;
-          return m < a.M ? reinterpret_cast<char*>(reinterpret_cast<T*>(a.C) + (size_t)m * a.ldc + c0) : nullptr;
-        }, nchunks(ncol - c0, 8, CPR));
-      }
-  } else {  // EPI_QKV: columns [q | k | v], each D = H * HD wide (HD == 64); q and k get RoPE
-    if (swap) {
-      constexpr int CW = fitw(WTN, SB / 64), CPR = CW / 8;
-      static_assert(CW % 64 == 0, "whole heads per staged block");
-      const bool rope = a.rope_cos != nullptr;
-      float* tcos = PRE ? reinterpret_cast<float*>(L + NST) : reinterpret_cast<float*>(reinterpret_cast<char*>(L) + 4 * SB);
-      float* tsin = tcos + BM * 32;
-      if (rope && !PRE) {
-        // RoPE tables of the tile's rows, cos in stage 0 and sin in stage 1 ([BM][32] floats each),
-        // NB 16-byte pieces of each per thread at a time: all of them (one round trip) up to 192
-        // rows, else four (the positions were loaded before the K loop)
-        constexpr int NB = NT <= 6 ? NT : 4;
-#pragma unroll
-        for (int k0 = 0; k0 < NT; k0 += NB) {
-          float4 tc[NB], ts[NB];
-#pragma unroll
-          for (int k = 0; k < NB; k++) {
-            if (k0 + k >= NT) break;
-            const int q = (tid + 256 * (k0 + k)) & 7;
-            tc[k] = *reinterpret_cast<const float4*>(a.rope_cos + pp[k0 + k] * 32 + 4 * q);
-            ts[k] = *reinterpret_cast<const float4*>(a.rope_sin + pp[k0 + k] * 32 + 4 * q);
-          }
-#pragma unroll
-          for (int k = 0; k < NB; k++) {
-            if (k0 + k >= NT) break;
-            const int it = tid + 256 * (k0 + k), r = it >> 3, q = it & 7;
-            *reinterpret_cast<float4*>(tcos + r * 32 + 4 * (q ^ rope_sw(r))) = tc[k];
-            *reinterpret_cast<float4*>(tsin + r * 32 + 4 * (q ^ rope_sw(r))) = ts[k];
-          }
-        }
-      }
-      float4 bx[FN][4] = {};
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) if constexpr (HB) bx[j][g] = bias4(cbase + j * 32 + 8 * g + 4 * hi);
-      if (rope && !PRE) __syncthreads();                  // tables complete
-      T* dst = reinterpret_cast<T*>(cbase < D ? a.Q : a.Kt) + (cbase % D);
-#pragma unroll
-      for (int i = 0; i < FM; i++) {
-        const int r = wm * WTM + i * 32 + l32;            // row within the tile
-#pragma unroll
-        for (int cp = 0; cp < WTN / CW; cp++) {
-#pragma unroll
-          for (int jp = cp * CW / 32; jp < (cp + 1) * CW / 32; jp += 2)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const int dd = 8 * g + 4 * hi;
-              const float4 x0 = bx[jp][g], x1 = bx[jp + 1][g];
-              const float4 a1 = av4(i, jp, g), a2 = av4(i, jp + 1, g);
-              const float p1[4] = {ab(a1.x, x0.x), ab(a1.y, x0.y), ab(a1.z, x0.z), ab(a1.w, x0.w)};
-              const float p2[4] = {ab(a2.x, x1.x), ab(a2.y, x1.y), ab(a2.z, x1.z), ab(a2.w, x1.w)};
-              float o1[4], o2[4];
-              if (rope) {
-                // rotate_half partners (d, d + 32) of a head are blocks jp, jp + 1 of one lane
-                const int tq = r * 32 + 4 * ((dd >> 2) ^ rope_sw(r));
-                const f32x4_t cs = *reinterpret_cast<const f32x4_t*>(tcos + tq);
-                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(tsin + tq);
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                  // explicit fused forms: left to contraction, different tile shapes could round
-                  // these differently
-                  o1[u] = fmaf(p1[u], cs[u], -(p2[u] * sn[u]));
-                  o2[u] = fmaf(p2[u], cs[u], p1[u] * sn[u]);
-                }
-              } else {
-#pragma unroll
-                for (int u = 0; u < 4; u++) { o1[u] = p1[u]; o2[u] = p2[u]; }
-              }
-              put8(l32, jp * 32 - cp * CW + dd, CPR, o1[0], o1[1], o1[2], o1[3]);
-              put8(l32, jp * 32 - cp * CW + 32 + dd, CPR, o2[0], o2[1], o2[2], o2[3]);
-            }
-          flush(CPR, [&](int rr) -> char* {
-            const int m = rbase + i * 32 + rr;
-            return m < a.M ? reinterpret_cast<char*>(dst + (size_t)m * a.ldqk + cp * CW) : nullptr;
-          }, CPR);
-        }
-      }
-    } else {
-      // V^T[c - 2D][row]: lane holds four consecutive rows of one column per e / 4; staged as
-      // [column][row] blocks of 32 columns x CW rows, streamed out along rows of V^T (chunks that
-      // start past row M are not written)
-      constexpr int CW = fitw(WTM, SB / 64), CPR = CW / 8;
-      float bvs[FN];                                       // loaded before the first store
-#pragma unroll
-      for (int j = 0; j < FN; j++) {
-        const int n = cbase + j * 32 + l32;
-        bvs[j] = HB && a.bias && n < a.N ? a.bias[n] : 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < FN; j++) {
-        const float bv = bvs[j];
-        const float cv = LNC ? lcs[cbase - n0 + j * 32 + l32] : 0.f;
-#pragma unroll
-        for (int cp = 0; cp < WTM / CW; cp++) {
-#pragma unroll
-          for (int i = cp * CW / 32; i < (cp + 1) * CW / 32; i++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              // element 4 g + u is row 32 i + 8 g + 4 hi + u of the wave's tile part; that row's mean
-              // and rstd come from the table
-              float v[4];
-#pragma unroll
-              for (int u = 0; u < 4; u++) v[u] = acc[i][j][4 * g + u];
-              if constexpr (LNC) {
-                const int r4 = wm * WTM + 32 * i + 8 * g + 4 * hi;
-                const float4 m4 = *reinterpret_cast<const float4*>(lrm + r4);
-                const float4 q4 = *reinterpret_cast<const float4*>(lrm + BMP + r4);
-                v[0] = __fmul_rn(fmaf(-m4.x, cv, v[0]), q4.x);
-                v[1] = __fmul_rn(fmaf(-m4.y, cv, v[1]), q4.y);
-                v[2] = __fmul_rn(fmaf(-m4.z, cv, v[2]), q4.z);
-                v[3] = __fmul_rn(fmaf(-m4.w, cv, v[3]), q4.w);
-              }
-              put8(l32, i * 32 - cp * CW + 8 * g + 4 * hi, CPR, ab(v[0], bv), ab(v[1], bv), ab(v[2], bv), ab(v[3], bv));
-            }
-          const int r0 = rbase + cp * CW;
-          flush(CPR, [&](int rr) -> char* {
-            const int nn = cbase + j * 32 + rr;
-            return nn < a.N ? reinterpret_cast<char*>(reinterpret_cast<T*>(a.Vt) + (size_t)(nn - 2 * D) * a.ldv + r0) : nullptr;
-          }, nchunks(a.M - r0, 8, CPR));
-        }
-      }
-    }
-  }
+// A row split in one launch: the tiles of rows [0, split) in the first tile shape (a: those rows,
+// nmain tiles, workgroups 0 .. nmain - 1), then the tiles of the remaining rows in the second
+// (b: the same GEMM from row split on).  Workgroups are dispatched in order of their index, so the
+// smaller tiles of the second shape start last and fill the CUs that the first shape's partial last
+// round leaves idle, where a second launch would wait for the first to finish.  Every output keeps
+// its K order, so the results are those of either shape alone.  Two workgroups per CU (both shapes
+// fit 80 KB of LDS and 256 registers).
+template <int BM, int BN, int WM, int WN, int LOOP, int BM2, int BN2, int WM2, int WN2, int LOOP2, int EPI>
+__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_xl_pair(
+    const GemmArgs a, const GemmArgs b, int nmain) {
+  constexpr int C1 = XlLds<BM, BN, EPI, LOOP>::chunks, C2 = XlLds<BM2, BN2, EPI, LOOP2>::chunks;
+  static_assert((C1 > C2 ? C1 : C2) * 16 <= 80 * 1024, "two workgroups per CU");
+  __shared__ u32x4_t L[C1 > C2 ? C1 : C2];
+  if ((int)blockIdx.x < nmain) xl_tile<BM, BN, WM, WN, EPI, ACT_NONE, false, LOOP, false>(a, blockIdx.x, L);
+  else xl_tile<BM2, BN2, WM2, WN2, EPI, ACT_NONE, false, LOOP2, false>(b, (int)blockIdx.x - nmain, L);
 }
 
 // GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
@@ -1726,6 +1052,32 @@ static void launch_xl_cfg(int epi, const GemmArgs& a, int cfg, hipStream_t st) {
   }
 }
 
+// Row splits that run as one launch (k_gemm_xl_pair): 192x128 tiles (two per CU) over the first
+// rows, then 128x64 or 128x128 tiles over the rest, for the plain store and the GeGLU epilogue
+// without bias, activation or LayerNorm fold.  The second shape's tiles take the three-A-buffer
+// loop, as they would in a launch of their own with two workgroups per CU.  Returns false for any
+// other split (which then runs as two launches).
+static bool launch_xl_pair(int epi, const GemmArgs& h, const GemmArgs& t, int cfg, int tail, hipStream_t st) {
+  if (cfg != 7 || (tail != 8 && tail != 3) || (epi != EPI_STORE && epi != EPI_GEGLU) || h.bias || h.act != ACT_NONE ||
+      ln_fold(h))
+    return false;
+  const int nmain = ((h.M + 191) / 192) * ((h.N + 127) / 128);
+  const int bn2 = tail == 8 ? 64 : 128;
+  const dim3 grid((unsigned)(nmain + ((t.M + 127) / 128) * ((t.N + bn2 - 1) / bn2)));
+  if (tail == 8) {
+    if (epi == EPI_STORE)
+      LAYA_LAUNCH((k_gemm_xl_pair<192, 128, 2, 2, 0, 128, 64, 4, 1, 1, EPI_STORE>), grid, dim3(256), 0, st, h, t, nmain);
+    else
+      LAYA_LAUNCH((k_gemm_xl_pair<192, 128, 2, 2, 0, 128, 64, 4, 1, 1, EPI_GEGLU>), grid, dim3(256), 0, st, h, t, nmain);
+  } else {
+    if (epi == EPI_STORE)
+      LAYA_LAUNCH((k_gemm_xl_pair<192, 128, 2, 2, 0, 128, 128, 2, 2, 1, EPI_STORE>), grid, dim3(256), 0, st, h, t, nmain);
+    else
+      LAYA_LAUNCH((k_gemm_xl_pair<192, 128, 2, 2, 0, 128, 128, 2, 2, 1, EPI_GEGLU>), grid, dim3(256), 0, st, h, t, nmain);
+  }
+  return true;
+}
+
 // Split-K reduction: out = epilogue(sum over the ks partial slices in slice order + bias), four
 // columns per thread.  EPI_RESID adds into the fp32 residual X; EPI_STORE applies the activation
 // and stores bf16.
@@ -1836,8 +1188,10 @@ void launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
       if (split > 0 && gemm_split_valid(epi, a, cfg, split, tail)) {
         GemmArgs head = a;
         head.M = split;
+        const GemmArgs rest = rows_from(a, split);
+        if (launch_xl_pair(epi, head, rest, cfg, tail, st)) return;
         launch_xl_cfg(epi, head, cfg, st);
-        launch_xl_cfg(epi, rows_from(a, split), tail, st);
+        launch_xl_cfg(epi, rest, tail, st);
         return;
       }
       if (!xl_cfg_fits(epi, a, cfg)) cfg = gemm_pick(epi, a);

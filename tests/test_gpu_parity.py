@@ -101,8 +101,10 @@ def test_gemm_vs_torch(dtype, cfg, M, N, K):
         le.gemm_config(lib, prev)
 
 
-# row splits: rows [split, M) in a second launch with another tile shape (split >= M: one launch)
-@pytest.mark.parametrize("cfg,split,tail", [(0, 256, 3), (4, 192, 2), (3, 128, 1), (0, 264, 4), (5, 160, 3)])
+# row splits: rows [split, M) in a second launch with another tile shape (split >= M: one launch);
+# 192x128 tiles followed by 128x64 or 128x128 ones run as one launch (k_gemm_xl_pair)
+@pytest.mark.parametrize("cfg,split,tail", [(0, 256, 3), (4, 192, 2), (3, 128, 1), (0, 264, 4), (5, 160, 3),
+                                            (7, 192, 8), (7, 192, 3), (7, 384, 8)])
 @pytest.mark.parametrize("M,N,K", [(300, 384, 192), (513, 1024, 2624), (200, 256, 320)])
 def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
     lib = le.load_library()
@@ -113,6 +115,41 @@ def test_gemm_row_split_vs_torch(cfg, split, tail, M, N, K):
     finally:
         le.gemm_split(lib, 0)
         le.gemm_config(lib, prev)
+
+
+@pytest.mark.parametrize("split,tail,M,N,K", [
+    (192, 8, 300, 384, 192), (192, 3, 300, 384, 192), (192, 8, 1000, 1024, 1024), (192, 3, 1000, 1024, 1024),
+    (576, 8, 1000, 1024, 1024), (576, 3, 1000, 1024, 1024), (192, 8, 4100, 640, 320), (576, 3, 4100, 640, 320),
+    (4032, 8, 4100, 640, 320), (4032, 3, 4100, 640, 320)])
+def test_gemm_pair_launch_bit_identical(split, tail, M, N, K):
+    """A row split of 192x128 tiles followed by 128x64 or 128x128 tiles, on a plain store without
+    bias or activation, runs as one launch (k_gemm_xl_pair: the first shape's tiles, then the
+    second's).  Its output must equal, bit for bit, a single launch of either shape, and the
+    product in fp64 within the bf16 bound."""
+    import torch
+    lib = le.load_library()
+    g = torch.Generator(device="cpu").manual_seed(M + 3 * N + 7 * K + split)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+
+    def run(cfg, sp=0, tl=-1):
+        C = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        prev = le.gemm_config(lib, cfg)
+        le.gemm_split(lib, sp, tl)
+        try:
+            le.gemm(lib, A, W, C)
+        finally:
+            le.gemm_split(lib, 0)
+            le.gemm_config(lib, prev)
+        torch.cuda.synchronize()
+        return C.cpu()
+
+    paired = run(7, split, tail)
+    for single in (run(7), run(tail)):
+        assert torch.equal(paired.view(torch.int16), single.view(torch.int16))
+    ref = A.cpu().double() @ W.cpu().double().T
+    err = ((paired.double() - ref).abs() - 2.0 ** -8 * ref.abs()).max().item()
+    assert err < 1e-5 * max(1.0, K ** 0.5), err
 
 
 # 128x128 tiles run the three-A-buffer K loop when the grid has more tiles than the chip has CUs
@@ -544,7 +581,8 @@ def test_tile_configs_bit_identical():
     """Every bf16 tile configuration runs the same K order through the same MFMA instruction, so the
     whole pass (all 28 layers of ModernBERT-large, 32 questions of the b32 x s512 batch, split into
     two passes) must give bit-identical outputs whichever tiles the GEMMs use, also when a GEMM's
-    rows are split over two launches with different tiles."""
+    rows are split over two launches with different tiles, or over the two tile shapes of one
+    launch (192x128 then 128x64 or 128x128 tiles: the GeGLU GEMMs)."""
     e = engine("large", "bf16", LAYA_GRAPHS=0)
     b = wl.c3(0)
     prev = le.gemm_config(e.lib, -1)
@@ -555,7 +593,7 @@ def test_tile_configs_bit_identical():
             lo, ac = e.forward_flat(*b.flat())
             assert np.array_equal(lo, ref_lo) and np.array_equal(ac, ref_ac), cfg
         # row splits: large tiles over the first rows, another shape over the rest
-        for cfg, split, tail in ((0, 1024, 3), (4, 960, 2), (0, 4096, 1)):
+        for cfg, split, tail in ((0, 1024, 3), (4, 960, 2), (0, 4096, 1), (7, 1536, 8), (7, 4032, 3)):
             le.gemm_config(e.lib, cfg)
             le.gemm_split(e.lib, split, tail)
             lo, ac = e.forward_flat(*b.flat())
