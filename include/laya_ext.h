@@ -87,9 +87,12 @@ int laya_ext_hbm_copy(const void* src, void* dst, size_t bytes, void* stream);
 int laya_ext_gemm_config(int cfg);
 
 /* Row split used with the pinned configuration: rows [split_rows, M) of every later pinned launch
- * run as a second launch with tile configuration cfg_tail (0..8); split_rows 0 removes the split.
+ * run with tile configuration cfg_tail (0..8), in a second launch, or in the same launch after the
+ * first configuration's tiles when that is 192x128 (7) and cfg_tail 128x64 (8) or 128x128 (3) on a
+ * store without bias or activation (or a GeGLU GEMM of the engine); split_rows 0 removes the split.
  * A split the shape cannot take (split_rows >= M, not a multiple of 8, a tail configuration the
- * shape cannot use) runs as one launch.  Returns 0, or -2 for an invalid value. */
+ * shape cannot use) runs as one launch of the first configuration.  Results are the same bits in
+ * every case.  Returns 0, or -2 for an invalid value. */
 int laya_ext_gemm_split(int split_rows, int cfg_tail);
 
 /* Split-K factor (0 or 1: none, up to 64) for later bf16 laya_ext_gemm calls, process-wide: K
