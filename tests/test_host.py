@@ -8,6 +8,8 @@ import tempfile
 
 import numpy as np
 import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from layamd_amd import checkpoint as ck
 from layamd_amd import engine as le
@@ -95,17 +97,23 @@ def test_layout_of_a_pass(host, q_tile, q_tile_global):
     cfg = ck.PRESETS["tiny"]
     b = wl.make_batch(cfg, [1, 64, 65, 200, 17, 128, 129, 256], [1, 3, 255, 12, 2, 1, 4, 2], seed=1)
     (p,) = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, q_tile=q_tile, q_tile_global=q_tile_global)
+    check_layout(b, p, cfg.pad_id, q_tile, q_tile_global)
+
+
+def check_layout(b, p, pad_id, q_tile, q_tile_global):
+    """The layout of one pass p of the questions of batch b (every question of b in the pass)."""
+    cfg = b.cfg
     rows8 = (b.lens + 7) // 8 * 8                                          # questions start on 8-row groups
     # the pass's rows are padded to a multiple of 64 (its graph bucket)
     assert p["B"] == b.B and p["T"] == up64(rows8.sum()) and p["valid"] == int(b.lens.sum())
     soff = np.concatenate([[0], np.cumsum(rows8)])
     assert np.array_equal(p["soff"], soff)
     tail = slice(soff[-1], p["T"])                                         # bucket padding rows
-    assert np.all(p["ids"][tail] == cfg.pad_id) and np.all(p["pos"][tail] == 0) and np.all(p["seq"][tail] == b.B - 1)
+    assert np.all(p["ids"][tail] == pad_id) and np.all(p["pos"][tail] == 0) and np.all(p["seq"][tail] == b.B - 1)
     for i in range(b.B):
         r = slice(soff[i], soff[i + 1])
         assert np.array_equal(p["ids"][r][:b.lens[i]], b.ids[i])
-        assert np.all(p["ids"][r][b.lens[i]:] == cfg.pad_id)               # padding rows: pad token
+        assert np.all(p["ids"][r][b.lens[i]:] == pad_id)                   # padding rows: pad token
         assert np.array_equal(p["pos"][r], np.arange(rows8[i]))
         assert np.all(p["seq"][r] == i)
         assert soff[i] % 8 == 0
@@ -147,6 +155,38 @@ def test_layout_of_a_pass(host, q_tile, q_tile_global):
             seen[gi] += 1
             assert soff[seq] <= p["grow"][gi] < soff[seq] + b.lens[seq]
     assert np.all(seen[:nmk] == 1) and np.all(seen[nmk:KT] == 0) and np.all(seen[KT:] == 1)
+    del cfg
+
+
+@settings(max_examples=80, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(data=st.data())
+def test_layout_properties_of_random_batches(host, data):
+    """The layout invariants of test_layout_of_a_pass on random batches (1-12 questions of 1-320
+    tokens, 1-255 markers, both query tilings), planned into one pass or, under tighter row,
+    question and gathered-row caps, several: the passes take the questions in order, each within
+    its caps, and each pass's layout holds for its own questions."""
+    cfg = ck.PRESETS["tiny"]
+    n = data.draw(st.integers(1, 12), label="questions")
+    lens = data.draw(st.lists(st.integers(1, 320), min_size=n, max_size=n), label="lens")
+    nm = data.draw(st.lists(st.integers(1, 255), min_size=n, max_size=n), label="markers")
+    q_tile, q_tile_global = data.draw(st.sampled_from([(64, 64), (64, 128), (128, 128)]), label="tiles")
+    rows_cap = data.draw(st.sampled_from([320, 640, 1024, 65536]), label="pass_tokens")
+    seqs_cap = data.draw(st.sampled_from([1, 3, 512]), label="max_seqs")
+    grows_cap = data.draw(st.sampled_from([257, 512, 32768]), label="max_grows")
+    b = wl.make_batch(cfg, lens, nm, seed=data.draw(st.integers(0, 1000), label="seed"))
+    ps = plan(host, *b.flat(), max_len=320, pad_id=cfg.pad_id, pass_tokens=rows_cap, max_seqs=seqs_cap,
+              max_grows=grows_cap, q_tile=q_tile, q_tile_global=q_tile_global)
+    assert ps is not None
+    nxt = 0
+    for p in ps:
+        assert p["first"] == nxt and p["B"] >= 1
+        sub = b.subset(range(nxt, nxt + p["B"]))
+        rows8 = int(np.sum((sub.lens + 7) // 8 * 8))
+        assert p["B"] <= seqs_cap and (p["B"] == 1 or rows8 <= rows_cap)
+        assert p["B"] == 1 or up64(int(sub.nmark.sum())) + p["B"] <= max(grows_cap, 257)
+        check_layout(sub, p, cfg.pad_id, q_tile, q_tile_global)
+        nxt += p["B"]
+    assert nxt == n
 
 
 def test_pass_splitting(host):
