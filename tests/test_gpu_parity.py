@@ -420,6 +420,43 @@ def test_packing_and_permutation_invariance(precision):
 
 
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_tiny_random_batches_vs_oracle(precision):
+    """Random calls on the tiny model (1-10 questions of 1-320 tokens with 1-255 markers and random
+    question types; a fixed sequence of examples, so every run checks the same calls) against the
+    CPU oracle with the bars of test_tiny_extremes_vs_oracle, and each question alone giving the
+    bits it has inside the call."""
+    from hypothesis import given, settings
+    from hypothesis import strategies as st
+    from oracle import model as om
+    cfg, W = ck.load_checkpoint(checkpoint_dir("tiny"))
+    Wo = om.Weights(W)
+    e = engine("tiny", precision)
+
+    @settings(max_examples=25, deadline=None, derandomize=True, database=None)
+    @given(data=st.data())
+    def check(data):
+        n = data.draw(st.integers(1, 10), label="questions")
+        lens = data.draw(st.lists(st.integers(1, 320), min_size=n, max_size=n), label="lens")
+        nm = data.draw(st.lists(st.integers(1, 255), min_size=n, max_size=n), label="markers")
+        b = wl.make_batch(ck.PRESETS["tiny"], lens, nm, seed=data.draw(st.integers(0, 999), label="seed"))
+        print("random tiny %s: lens %s markers %s" % (precision, lens, nm), flush=True)
+        lo, ac = e.forward_flat(*b.flat())
+        ref_lo, ref_ac = om.run_per_question(Wo, ck.PRESETS["tiny"], b)
+        d = prob_delta(lo, ref_lo, b.nmark)
+        dl, dA = float(np.abs(lo - ref_lo).max()), float(np.abs(ac - ref_ac).max())
+        if precision == "fp32":
+            da = float((np.abs(ac - ref_ac) / np.maximum(1.0, np.abs(ref_ac))).max())
+            assert dl < 1e-4 and d < FP32_PROB and da < FP32_ACT, (d, dl, da)
+        else:
+            assert d < BF16_PROB and dl < BF16_TINY_LOGIT and dA < BF16_TINY_LOGIT, (d, dl, dA)
+        moff = np.concatenate([[0], np.cumsum(b.nmark)])
+        for i in range(n):
+            l1, a1 = e.forward_flat(*b.subset([i]).flat())
+            assert np.array_equal(l1, lo[moff[i]:moff[i + 1]]) and np.array_equal(a1[0], ac[i]), i
+    check()
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_tiny_extremes_vs_oracle(precision):
     """The limits of the interface against the CPU oracle: a question of the maximum length (320),
     one with the maximum of 255 markers, single-token and single-marker questions, in one call."""
