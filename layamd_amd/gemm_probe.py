@@ -28,7 +28,11 @@ on their tile configurations, the per-tile timeline its GEMM records (csrc/tile_
 shader clock the tiles ran at, prologue, K loop, the K loop's stage waits and the epilogue per tile,
 how the tiles' start times spread over the launch, and the K loop's MFMA rate against the rate the
 CU has at that clock (4 SIMDs x 1024 flop per cycle: one v_mfma_f32_32x32x16_bf16 per 32 cycles).
-With --M/--N/--K/--cfg given explicitly it traces that one shape (plain store).
+With --M/--N/--K/--cfg given explicitly it traces that one shape (plain store); --split R --tail C
+with --cfg 7 (C = 8 or 3) traces a row split that runs as one launch (k_gemm_xl_pair): per-tile
+figures of the first shape's tiles, the span and start spread of all, and when the tail tiles
+started and ended.  The b32 x s512 list includes the Wi shape's split at row 9408 (the tuner's
+plan for the GeGLU GEMM there).
 """
 import argparse
 import time
@@ -110,7 +114,9 @@ def c2(lib, shapes=C2_SHAPES, dtypes=None):
 # b32 x s512 pass on the tiles the tuner picks for them there (and 256x256 for the QKV shape)
 TRACE_C3 = [("QKV shape, store", False, 3072, 1024, 5), ("QKV shape, store", False, 3072, 1024, 0),
             ("out-proj, residual", True, 1024, 1024, 5), ("Wi shape, store", False, 5248, 1024, 7),
-            ("MLP-out, residual", True, 1024, 2624, 5)]
+            ("Wi shape, store", False, 5248, 1024, 7, 9408, 8), ("MLP-out, residual", True, 1024, 2624, 5)]
+# row splits that run as one launch (k_gemm_xl_pair): (first configuration, tail configuration)
+PAIRS = {(7, 8), (7, 3)}
 # (tile rows, tile columns, workgroups per CU) of the tile configurations
 TILES = {0: (256, 256, 1), 1: (256, 128, 1), 2: (128, 256, 1), 3: (128, 128, 2), 4: (192, 256, 1),
          5: (160, 256, 1), 6: (128, 192, 2), 7: (192, 128, 2), 8: (128, 64, 2)}
@@ -129,11 +135,16 @@ def tile_trace(M, cases):
     print("| GEMM (M = %d) | tile | tiles (rounds) | us per launch | span us | clock GHz | prologue us | K loop us "
           "| stage waits us | epilogue us | K loop MFMA rate at that clock | start spread us (p50, max) |" % M)
     print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---|")
-    for label, resid, N, K, cfg in cases:
+    for case in cases:
+        label, resid, N, K, cfg = case[:5]
+        split, tail = case[5:7] if len(case) > 5 else (0, -1)
+        # a split is traced only where it runs as one launch (one record per workgroup)
+        assert split == 0 or ((cfg, tail) in PAIRS and not resid and 0 < split < M), case
         A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
         W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
         C = torch.zeros(M, N, dtype=torch.float32 if resid else torch.bfloat16, device="cuda")
         le.gemm_config(lib, cfg)
+        le.gemm_split(lib, split, tail)
         for _ in range(3):
             le.gemm(lib, A, W, C, residual=resid)
         torch.cuda.synchronize()
@@ -144,11 +155,16 @@ def tile_trace(M, cases):
         le.gemm(lib, A, W, C, residual=resid)
         torch.cuda.synchronize()
         bm, bn, per_cu = TILES[cfg]
-        nt = ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
-        rec = np.zeros(8 * nt, np.uint64)
-        assert lib.laya_tile_trace_read(rec.ctypes.data, nt) == 0
-        r = rec.reshape(nt, 8).astype(np.float64)
-        assert (r[:, 7] > 0).all(), "a tile left no record"
+        nt = ((min(split or M, M) + bm - 1) // bm) * ((N + bn - 1) // bn)          # the first shape's tiles
+        ntt = 0
+        if split:
+            bm2, bn2, _ = TILES[tail]
+            ntt = ((M - split + bm2 - 1) // bm2) * ((N + bn2 - 1) // bn2)          # then the tail's
+        rec = np.zeros(8 * (nt + ntt), np.uint64)
+        assert lib.laya_tile_trace_read(rec.ctypes.data, nt + ntt) == 0
+        rall = rec.reshape(nt + ntt, 8).astype(np.float64)
+        assert (rall[:, 7] > 0).all(), "a tile left no record"
+        r = rall[:nt]                                       # per-tile figures: the first shape's tiles
         r0, r3 = r[:, 0], r[:, 1]
         dur_us = (r3 - r0) / 100.0                          # 100 MHz real-time clock
         ghz = r[:, 7].sum() / dur_us.sum() / 1e3
@@ -156,11 +172,20 @@ def tile_trace(M, cases):
         kloop = us(3)
         rate = 2.0 * bm * bn * K / (kloop * 1e-6) * per_cu        # flop/s of one CU in the K loop
         peak = 4 * 1024 * ghz * 1e9
-        start = (r0 - r0.min()) / 100.0
-        print("| %s %dx%dx%d | %dx%d%s | %d (%.2f) | %.1f | %.1f | %.2f | %.2f | %.2f | %.2f (%.0f%%) | %.2f | %.0f%% | %.1f, %.1f |"
-              % (label, M, N, K, bm, bn, ", 2 per CU" if per_cu == 2 else "", nt, nt / (256.0 * per_cu), per_us,
-                 (r3.max() - r0.min()) / 100.0, ghz, us(2), kloop, us(5), 100 * us(5) / kloop, us(4), 100 * rate / peak,
-                 np.percentile(start, 50), start.max()), flush=True)
+        t0 = rall[:, 0].min()
+        start = (rall[:, 0] - t0) / 100.0
+        shape = "%dx%d%s" % (bm, bn, ", 2 per CU" if per_cu == 2 else "")
+        tiles = "%d (%.2f)" % (nt, nt / (256.0 * per_cu))
+        spread = "%.1f, %.1f" % (np.percentile(start, 50), start.max())
+        if split:
+            tst = start[nt:]
+            shape += " to row %d, then %dx%d" % (split, bm2, bn2)
+            tiles = "%d + %d" % (nt, ntt)
+            spread += "; tail tiles start %.1f-%.1f, end by %.1f" % (tst.min(), tst.max(), (rall[nt:, 1].max() - t0) / 100.0)
+        print("| %s %dx%dx%d | %s | %s | %.1f | %.1f | %.2f | %.2f | %.2f | %.2f (%.0f%%) | %.2f | %.0f%% | %s |"
+              % (label, M, N, K, shape, tiles, per_us, (rall[:, 1].max() - t0) / 100.0, ghz, us(2), kloop, us(5),
+                 100 * us(5) / kloop, us(4), 100 * rate / peak, spread), flush=True)
+    le.gemm_split(lib, 0)
     le.gemm_config(lib, -1)
 
 
@@ -177,11 +202,15 @@ def main():
                     help="after the engine launches, run torch.mm on the same operands as many times")
     ap.add_argument("--tile-trace", action="store_true",
                     help="per-tile timeline from liblaya_trace.so (python -m layamd_amd.build --tile-trace)")
+    ap.add_argument("--split", type=int, default=0,
+                    help="with --tile-trace and --cfg 7: rows from --split on in --tail tiles, in the same launch")
+    ap.add_argument("--tail", type=int, default=8)
     a, _ = ap.parse_known_args()
     if a.tile_trace:
         import sys
         explicit = any(x.split("=")[0] in ("--M", "--N", "--K", "--cfg") for x in sys.argv[1:])
-        tile_trace(a.M if explicit else 9664, [("store", False, a.N, a.K, a.cfg)] if explicit else TRACE_C3)
+        case = ("store", False, a.N, a.K, a.cfg) + ((a.split, a.tail) if a.split else ())
+        tile_trace(a.M if explicit else 9664, [case] if explicit else TRACE_C3)
         return
     lib = le.load_library()
     import torch
