@@ -709,11 +709,6 @@ __device__ __forceinline__ void xl_k_loop64d(f32x16_t (&acc)[FM][FN], const u32x
   LAYA_WAIT_VMCNT(0);                      // the refills past the last stage
 }
 
-// LOOP: the K loop.  0: two stage buffers (one workgroup per CU); 1 (128x128 tiles when the grid
-// puts two workgroups on a CU): three A buffers and two W buffers; 2 (128x128 tiles, grid of at most
-// one workgroup per CU): four stage buffers, two stages of lead.
-// LNX: the LayerNorm fold of GemmArgs.  With EPI_RESID the kernel writes Xh and the per-group
-// statistics; with EPI_STORE, EPI_QKV and EPI_GEGLU it applies the fold to its product.
 // LDS of one tile (16-byte chunks): the K stages (two whole stages; LOOP 1: three A buffers and two
 // W buffers; LOOP 2: four whole stages) and, for the QKV projection with two stages where it fits,
 // the RoPE tables of the tile's rows
@@ -726,8 +721,13 @@ struct XlLds {
   static constexpr int chunks = NST + (PRE ? BM * 16 : 0);
 };
 
-// One BM x BN output tile (tile `bid` of the GEMM; with EPI_PARTIAL, bid also selects the K chunk),
-// computed by the 256 threads of the calling workgroup in the LDS array L (XlLds chunks)
+// One BM x BN output tile (tile bid0 of the GEMM; with EPI_PARTIAL, bid0 also selects the K chunk),
+// computed by the 256 threads of the calling workgroup in the LDS array L (XlLds chunks).
+// LOOP: the K loop.  0: two stage buffers (one workgroup per CU); 1 (128x128 tiles when the grid
+// puts two workgroups on a CU): three A buffers and two W buffers; 2 (128x128 tiles, grid of at most
+// one workgroup per CU): four stage buffers, two stages of lead.
+// LNX: the LayerNorm fold of GemmArgs.  With EPI_RESID the kernel writes Xh and the per-group
+// statistics; with EPI_STORE, EPI_QKV and EPI_GEGLU it applies the fold to its product.
 template <int BM, int BN, int WM, int WN, int EPI, int ACT, bool HB, int LOOP, bool LNX>
 __device__ __forceinline__ void xl_tile(const GemmArgs a, int bid0, u32x4_t* L) {
 #include "gemm_xl_tile.inc"
@@ -757,8 +757,6 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   else xl_tile<BM2, BN2, WM2, WN2, EPI, ACT_NONE, false, LOOP2, false>(b, (int)blockIdx.x - nmain, L);
 }
 
-// GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
-// build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
 // The achievable bf16 MFMA rate of the chip at the clock it holds under MFMA load: every wave
 // issues v_mfma_f32_32x32x16_bf16 back to back on eight independent register accumulators, with
 // no memory traffic, and stores one value per lane at the end (so the work is kept).  32768 flop
@@ -822,6 +820,8 @@ static constexpr bool ln_fold_built(bool bias) {
   return EPI == EPI_RESID || EPI == EPI_QKV || (EPI == EPI_GEGLU && ACT == ACT_NONE) || (EPI == EPI_STORE && ACT == ACT_RELU);
 }
 
+// GEMMs without a bias run kernels without the bias code, except the QKV projection: its bias-free
+// build allocates registers worse (it spills at 256x256), so it keeps the bias code (adding 0)
 template <int BM, int BN, int WM, int WN, int EPI, int ACT, int LOOP>
 static void launch_xl_ring(const GemmArgs& a, int tiles, hipStream_t st) {
   if (ln_fold(a)) {
