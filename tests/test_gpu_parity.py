@@ -33,9 +33,9 @@ FP32_HIDDEN = 1e-3
 FP32_PROB = 1e-4
 FP32_ACT = 1e-3
 # bf16 drift budgets (see the module docstring).  Measured on MI355X: the engine's per-layer drift
-# is 0.6-1.2x the reference's bf16 drift, and its logit and act deviations 0.2-1.3x the
+# is 0.6-1.2x the reference's bf16 drift, and its logit and act deviations 0.2-1.8x the
 # reference's (ModernBERT-large b1 x s128, every question of the b32 x s512 and b16 x s1024
-# batches, samples of the b64 varlen batch); the worst layer of any question uses 0.28-0.37 of its
+# batches, all of the b64 varlen batch); the worst layer of any question uses 0.28-0.42 of its
 # budget.  The embedding output is fp32 in both (the engine keeps the token embeddings in fp32), so
 # the reference's bf16 drift there is 0 and the engine's about 1e-7.  The floor, 2^-6 of the row
 # RMS, is one bf16 rounding of a layer's GEMM input: it matters only where the reference's own
