@@ -1,5 +1,6 @@
-"""The measurement tools that the committed kernel-trace summaries come from, on synthetic input
-(no GPU): layamd_amd/trace_table.py reads a kernel trace per stage of the pass."""
+"""The measurement tools behind the committed profile summaries, without a GPU:
+layamd_amd/trace_table.py reading a synthetic kernel trace per stage of the pass, and the traffic
+record that bench.py reports belonging to the GEMM sources in the tree."""
 import csv
 import json
 import subprocess
@@ -75,6 +76,22 @@ def test_trace_table_rejects_a_trace_without_the_sequence(tmp_path):
     seq.write_text("\n".join(SEQ + ["enc:extra"]) + "\n")
     r = subprocess.run([sys.executable, "-m", "layamd_amd.trace_table", str(tr), str(seq)], capture_output=True, text=True)
     assert r.returncode != 0 and "no pass of 5 kernels" in r.stderr
+
+
+def test_recorded_traffic_belongs_to_these_gemm_sources():
+    """bench.py reports the dominant GEMM's fabric traffic from the counter runs recorded in
+    profiles/ only for the GEMM sources those runs measured (their hash is recorded beside the
+    figure).  The committed record must belong to the committed sources: a change to the GEMM
+    sources needs the two counter runs again."""
+    import importlib.util
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_module", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    rec, note = bench.measured_traffic("enc:gemm_mlp_in_geglu")
+    assert rec is not None, note
+    assert rec > 81e6                     # at least the operands and output (81.2 MB per launch)
 
 
 if __name__ == "__main__":
